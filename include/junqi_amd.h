@@ -1,0 +1,197 @@
+/*
+ * junqi_amd.h -- C ABI of the MI355X batched Junqi environment.
+ *
+ * One handle owns N games in HBM. Every entry point returns 0 on success or a
+ * negative JQ_E* code (message via jq_last_error()); nothing throws or exits.
+ * Device pointers are plain addresses of caller memory (e.g. torch tensors);
+ * `stream` is a hipStream_t passed as void* (NULL = default stream). No entry
+ * point synchronises the device unless it says so.
+ *
+ * Each declaration names the reference interface it replaces (paths relative
+ * to the reference repository).
+ */
+#ifndef JUNQI_AMD_H
+#define JUNQI_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JQ_NUM_CELLS 289
+#define JQ_NUM_ON_BOARD 129
+#define JQ_NUM_PIDS 120
+#define JQ_OBS_CHANNELS 317
+#define JQ_OBS_GLOBALS 28
+#define JQ_ACTION_DIM 16641        /* 129 * 129 compact canonical actions */
+#define JQ_MASK_WORDS 521          /* 32-bit words per packed canonical mask row */
+#define JQ_AUX_PLANES 6            /* continuous planes carried in fp32 by the u8 format */
+#define JQ_MAX_LEGAL 3200          /* per-env upper bound on legal actions (25 pieces x 128) */
+
+/* error codes */
+#define JQ_OK 0
+#define JQ_E_ARG (-1)      /* bad argument (null, range, shape) */
+#define JQ_E_STATE (-2)    /* handle not ready (tables / pool missing) */
+#define JQ_E_HIP (-3)      /* HIP runtime error */
+#define JQ_E_OOM (-4)      /* device allocation failed */
+
+/* observation output formats */
+#define JQ_OBS_F32 0       /* (N,317,17,17) float32, the reference layout */
+#define JQ_OBS_BF16 1      /* (N,317,17,17) bfloat16 = round-to-nearest-even of the f32 */
+#define JQ_OBS_U8 2        /* (N,317,17,17) uint8 codes + (N,6,17,17) float32 aux planes */
+
+/* action formats for jq_step */
+#define JQ_ACT_WORLD 0     /* src_flat*289 + dst_flat in the world frame */
+#define JQ_ACT_CANONICAL 1 /* compact canonical id src_c*129 + dst_c of the acting seat */
+
+typedef struct jq_env jq_env;
+
+/* Last error message of the calling thread. */
+const char *jq_last_error(void);
+/* Library version string. */
+const char *jq_version(void);
+
+/* Create / destroy N games on `device`. Replaces junqi_cuda.DeviceGameStateBatch
+ * (src/env/cuda/src/bindings.cpp:462-560) and DeviceObservation*Batch. */
+int jq_create(jq_env **out, int32_t num_envs, int32_t max_num_moves, int32_t show_mode, int32_t device);
+int jq_destroy(jq_env *env);
+int32_t jq_num_envs(const jq_env *env);
+
+/* Zobrist tables as numpy's PCG64 stream draws them (junqi_core/_zobrist.py:80-106),
+ * host pointer, `count` uint64 values. Replaces junqi_cuda.upload_zobrist_tables
+ * (junqi_rl/gpu_world.py:77-94). Must precede any reset. */
+int jq_upload_zobrist(jq_env *env, const uint64_t *host_table, int64_t count);
+
+/* Recency table float32[4][4096] (observation.py:1552-1567 values). Host pointer. */
+int jq_upload_recency(jq_env *env, const float *host_lut);
+
+/* Setup pool (pool_size,120) int8 piece types per pid, host pointer. Replaces
+ * junqi_cuda.upload_setup_pool (junqi_rl/gpu_rollout.py:588-652). */
+int jq_upload_setup_pool(jq_env *env, const int8_t *host_pool, int32_t pool_size);
+
+/* Start every env from the given lineups ((N,120) int8 piece types per pid, host
+ * pointer): GameState.new_game + BeliefTensor.initial for all four observers.
+ * Replaces GpuRollout.reset's copy_from_host path (junqi_rl/gpu_rollout.py:690-744). */
+int jq_reset_lineups(jq_env *env, const int8_t *host_lineups, void *stream);
+
+/* Host-side lineup generation identical to junqi_core.setup.generate_random_setup
+ * (setup.py:162-258) under random.Random(seed_base + i), then jq_reset_lineups.
+ * This is GpuRollout.reset(seed_base) (gpu_rollout.py:690-744). Synchronises. */
+int jq_reset_seeded(jq_env *env, int64_t seed_base, void *stream);
+/* The lineups jq_reset_seeded would use, without touching the device. */
+int jq_generate_lineups(int64_t seed_base, int32_t count, int8_t *host_out);
+/* The setup pool of junqi_rl/gpu_rollout.py:255-275: pool_size setups drawn from
+ * one random.Random(seed) stream, (pool_size,120) int8 piece types per pid. */
+int jq_generate_pool(int64_t seed, int32_t pool_size, int8_t *host_out);
+/* Copy of the host-built constant board tables (struct jq::Tables of
+ * junqi_amd/csrc/jq_topology.h), for inspection by tests. */
+int jq_board_tables(void *host_out, int64_t nbytes);
+
+/* Reset terminated envs from the pool, picking entry hash(env, seed) % pool_size
+ * (src/env/cuda/src/game_state.cu:2936-3102). Replaces reset_terminated_envs
+ * (gpu_rollout.py:1007-1028). `mask` (device uint8, N) optionally limits it. */
+int jq_reset_terminated(jq_env *env, int64_t seed, void *stream);
+
+/* Apply one ply per env. actions: device int32 (N) in `action_format`; acting:
+ * device int8 (N) seat per env (NULL = current turn; required for canonical ids).
+ * Outputs (device, any may be NULL): valid u8, event i8, terminated u8, winner i8,
+ * draw u8, flag_captured u8, seats_died u8 bitmask, reward f32 (acting team +-1 on
+ * the ply that ends the game), world_action i32.
+ * Replaces step_device (game_state.cu:2731-2797, bindings.cpp:1044-1073) and
+ * GpuWorld.step_batch (gpu_world.py:223-253). Terminated envs are skipped. */
+int jq_step(jq_env *env, const int32_t *actions, const int8_t *acting, int32_t action_format,
+            uint8_t *valid, int8_t *event, uint8_t *terminated, int8_t *winner, uint8_t *draw,
+            uint8_t *flag_captured, uint8_t *seats_died, float *reward, int32_t *world_action,
+            void *stream);
+
+/* Legal actions of `acting` (device int8 N; NULL = current turn) for every env.
+ * counts: device int32 (N); offsets: device int32 (N+1), exclusive scan of counts;
+ * values: device int32 (capacity >= N*JQ_MAX_LEGAL), per-env ascending world ids
+ * src*289+dst (move_gen.py:1199 order); mask_words: device int32 (N, 521) packed
+ * canonical compact mask; mask_bool: device uint8 (N, 16641) (gpu_rollout.py:1220).
+ * Any output may be NULL (offsets/values need counts). Replaces
+ * legal_action_ids_batch_csr (game_state.cu:1892-1962) and
+ * legal_mask_canonical_batch (game_state.cu:2291-2508). */
+int jq_legal(jq_env *env, const int8_t *acting, int32_t *counts, int32_t *offsets, int32_t *values,
+             int32_t *mask_words, uint8_t *mask_bool, void *stream);
+
+/* Observation of `observer` (device int8 N; NULL = current turn) in that seat's
+ * canonical frame. fmt JQ_OBS_*; spatial: device (N,317,17,17) of the format's
+ * element type; aux: device float (N,6,17,17) for JQ_OBS_U8 (else NULL);
+ * global: device float (N,28). all_seats != 0 writes (N,4,...) for observers
+ * 0..3 and ignores `observer`. Replaces build_observation_single_seat /
+ * build_observation_batch_resident (observation.cu:648-802). */
+int jq_observe(jq_env *env, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial,
+               float *aux, float *global, void *stream);
+
+/* The 256-entry float32 decode table of JQ_OBS_U8 codes (host pointer out). */
+int jq_obs_decode_table(float *host_out256);
+
+/* Sampler: world action per env drawn uniformly from its legal row with Philox4x32-10
+ * keyed (seed, ply) and counter (env) -- index = (u32 * count) >> 32. Needs the
+ * counts/offsets/values of jq_legal. Writes -1 for envs with no legal action. */
+int jq_sample_uniform(jq_env *env, const int32_t *counts, const int32_t *offsets, const int32_t *values,
+                      uint64_t seed, uint64_t ply, int32_t *actions_out, void *stream);
+
+/* One fused env-step for the whole batch: sample (if actions == NULL) -> step ->
+ * auto-reset terminated envs from the pool -> legal (counts/offsets/values/mask) ->
+ * observation of the new acting seat. Buffers as in the calls above. */
+int jq_env_step(jq_env *env, const int32_t *actions, uint64_t sample_seed, uint64_t ply,
+                int64_t reset_seed, int32_t *counts, int32_t *offsets, int32_t *values,
+                int32_t *mask_words, int32_t obs_fmt, void *spatial, float *aux, float *global,
+                uint8_t *terminated, float *reward, int32_t *actions_out, void *stream);
+
+/* State import / export (host memory), one field at a time. Replaces
+ * DeviceGameStateBatch.copy_to_host / copy_from_host (bindings.cpp:73-198).
+ * jq_field_info gives the per-env element count and element size of a field. */
+enum jq_field {
+    JQ_F_CELL = 0,        /* int8  [289]   pid on the cell, -1 empty */
+    JQ_F_PTYPE = 1,       /* int8  [128]   PieceType per pid (-1 absent) */
+    JQ_F_POS = 2,         /* int16 [128]   flat cell, -1 dead/absent */
+    JQ_F_ZERO = 3,        /* int16 [128]   initial cell, -1 none */
+    JQ_F_MOVE_COUNT = 4,  /* int16 [128] */
+    JQ_F_ACTIVE_EAT = 5,  /* int16 [128] */
+    JQ_F_PASSIVE_SURV = 6,/* int16 [128] */
+    JQ_F_DEATH_REASON = 7,/* int8  [128]  -1 alive */
+    JQ_F_DEATH_STEP = 8,  /* int16 [128] */
+    JQ_F_DEATH_LOC = 9,   /* int16 [128] */
+    JQ_F_BELIEF = 10,     /* uint8 [4][128] belief row code per observer */
+    JQ_F_REMAINING = 11,  /* int8  [4][4][12] */
+    JQ_F_REM_TRACKED = 12,/* uint8 [4] bit s = remaining[s] tracked */
+    JQ_F_CM_DIRECT_LO = 13, JQ_F_CM_DIRECT_HI = 14, JQ_F_CM_DIRECT_TYPE = 15,
+    JQ_F_CM_LAST_DIRECT = 16, JQ_F_CM_OTHER_COUNT = 17, JQ_F_CM_CHAIN_LO = 18,
+    JQ_F_CM_CHAIN_HI = 19, JQ_F_CM_CHAIN_TYPE = 20, JQ_F_CM_LAST_CHAIN = 21,
+    JQ_F_CM_EATEN_LO = 22, JQ_F_CM_EATEN_HI = 23, JQ_F_CM_FLOOR = 24,
+    JQ_F_CM_FLOOR_STEP = 25,
+    JQ_F_CM_FLAGS = 26,   /* uint8 [4][128] bit0 is_gongb, bit1 not_gongb, bit2 attacked_by_known_gongb */
+    JQ_F_HIST = 27,       /* int32 [32] ring of src | dst<<16 */
+    JQ_F_HIST_META = 28,  /* int32 [1] count | head<<8 */
+    JQ_F_TURN = 29,       /* int8 */
+    JQ_F_TERMINATED = 30, /* uint8 */
+    JQ_F_WINNER = 31,     /* int8 -1/0/1 */
+    JQ_F_DRAW = 32,       /* uint8 */
+    JQ_F_SEAT_DEAD = 33,  /* uint8 bitmask */
+    JQ_F_FLAG_REV = 34,   /* uint8 bitmask */
+    JQ_F_MOVE_COUNTER = 35, /* int32 */
+    JQ_F_MSLC = 36,       /* int32 moves since last combat */
+    JQ_F_ZOBRIST = 37,    /* uint64 */
+    JQ_F_COUNT = 38
+};
+int jq_field_info(int32_t field, int32_t *elems_per_env, int32_t *elem_bytes);
+int jq_get_field(jq_env *env, int32_t field, void *host_dst);
+int jq_set_field(jq_env *env, int32_t field, const void *host_src);
+/* Device address of a state field (zero-copy views, e.g. turn_torch). */
+int jq_field_ptr(jq_env *env, int32_t field, void **dev_ptr);
+/* After jq_set_field edits: recompute every env's Zobrist hash and re-seed the
+ * four beliefs from the current board (GameState.__post_init__, state.py:346-483;
+ * BeliefTensor.initial, info_model.py:218-265). */
+int jq_finalize_import(jq_env *env, void *stream);
+
+/* Synchronise `stream`. */
+int jq_sync(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,14 @@
+"""MI355X-native batched four-player Junqi environment.
+
+The rules, legal-move generation, combat memory, beliefs and the 317-plane
+observation run as HIP kernels in ``_build/libjunqi_amd.so`` (C ABI declared in
+``include/junqi_amd.h``). Importing this package fails if that library is not
+built; there is no CPU implementation behind it.
+"""
+
+from . import _lib
+from ._lib import AUX_CHANNELS, JunqiError
+from .batch import JunqiBatch, decode_table, generate_lineups, generate_pool, recency_table, zobrist_stream
+
+__all__ = ["JunqiBatch", "JunqiError", "AUX_CHANNELS", "decode_table", "generate_lineups",
+           "generate_pool", "recency_table", "zobrist_stream", "_lib"]

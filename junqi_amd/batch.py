@@ -1,0 +1,274 @@
+"""Host handle over the HIP library: N games resident in HBM.
+
+``JunqiBatch`` owns one C-ABI handle and the torch device buffers its calls
+write. Torch provides device memory and the current HIP stream; every rule,
+legal move and observation is computed by the library's kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _lib as L
+from ._lib import check, lib
+
+DATA = Path(__file__).resolve().parent / "data"
+ZOBRIST_SEED = 0x4A554E51495F5A4F
+_ZOB_SHAPES = [(120, 14, 289), (4,), (4096,), (512,), (1,), (3,), (1,), (4,), (4,), (4,)]
+
+
+def zobrist_stream() -> np.ndarray:
+    """The Zobrist tables in draw order of junqi_core/_zobrist.py:80-106
+    (numpy PCG64, the reference's own dependency), as one uint64 array."""
+    rng = np.random.default_rng(ZOBRIST_SEED)
+    parts = [rng.integers(low=0, high=np.iinfo(np.uint64).max, size=s, dtype=np.uint64,
+                          endpoint=True).ravel() for s in _ZOB_SHAPES]
+    return np.ascontiguousarray(np.concatenate(parts))
+
+
+def recency_table() -> np.ndarray:
+    """float32[4][4096]: exp(-e/tau) for tau planes (32, 256, 64, 128), the values
+    junqi_core/observation.py:1561-1562 produces with numpy."""
+    lut = np.fromfile(DATA / "recency_lut_f32.bin", dtype="<f4")
+    if lut.size != 4 * 4096:
+        raise RuntimeError("corrupt recency table")
+    return np.ascontiguousarray(lut)
+
+
+def generate_lineups(seed_base: int, count: int) -> np.ndarray:
+    out = np.zeros((count, 120), dtype=np.int8)
+    check(lib.jq_generate_lineups(int(seed_base), int(count), out.ctypes.data))
+    return out
+
+
+def generate_pool(seed: int, size: int) -> np.ndarray:
+    out = np.zeros((size, 120), dtype=np.int8)
+    check(lib.jq_generate_pool(int(seed), int(size), out.ctypes.data))
+    return out
+
+
+def decode_table() -> np.ndarray:
+    out = np.zeros(256, dtype=np.float32)
+    check(lib.jq_obs_decode_table(out.ctypes.data))
+    return out
+
+
+class _CudaArrayView:
+    """__cuda_array_interface__ wrapper so torch can view library-owned memory."""
+
+    def __init__(self, ptr: int, shape: tuple[int, ...], typestr: str):
+        self.__cuda_array_interface__ = {"data": (int(ptr), False), "shape": tuple(shape),
+                                         "typestr": typestr, "version": 2}
+
+
+_TYPESTR = {(1, "i"): "|i1", (1, "u"): "|u1", (2, "i"): "<i2", (2, "u"): "<u2", (4, "i"): "<i4",
+            (8, "u"): "<u8"}
+_FIELD_KIND = {"hist": "i", "hist_meta": "i", "move_counter": "i", "mslc": "i", "zobrist": "u",
+               "belief": "u", "rem_tracked": "u", "cm_direct_lo": "u", "cm_direct_hi": "u",
+               "cm_direct_type": "u", "cm_chain_lo": "u", "cm_chain_hi": "u", "cm_chain_type": "u",
+               "cm_eaten_lo": "u", "cm_eaten_hi": "u", "cm_flags": "u", "terminated": "u", "draw": "u",
+               "seat_dead": "u", "flag_rev": "u"}
+
+
+class JunqiBatch:
+    """N four-player Junqi games on one GPU."""
+
+    def __init__(self, num_envs: int, *, show_mode: int = 2, max_num_moves: int = 4000,
+                 device: int = 0, setup_pool: np.ndarray | None = None, pool_seed: int = 42,
+                 pool_size: int = 10000):
+        if num_envs <= 0:
+            raise ValueError(f"num_envs must be positive, got {num_envs}")
+        if not torch.cuda.is_available():
+            raise RuntimeError("no GPU visible: junqi_amd runs on the device only")
+        self.n = int(num_envs)
+        self.show_mode = int(show_mode)
+        self.device = torch.device("cuda", device)
+        h = C.c_void_p()
+        with torch.cuda.device(self.device):
+            check(lib.jq_create(C.byref(h), self.n, int(max_num_moves), self.show_mode, int(device)))
+        self._h = h
+        z = zobrist_stream()
+        check(lib.jq_upload_zobrist(h, z.ctypes.data, z.size))
+        r = recency_table()
+        check(lib.jq_upload_recency(h, r.ctypes.data))
+        pool = generate_pool(pool_seed, pool_size) if setup_pool is None else np.ascontiguousarray(
+            setup_pool, dtype=np.int8).reshape(-1, 120)
+        self.upload_setup_pool(pool)
+        dev = self.device
+        self.counts = torch.zeros(self.n, dtype=torch.int32, device=dev)
+        self.offsets = torch.zeros(self.n + 1, dtype=torch.int32, device=dev)
+        self.values = torch.zeros(self.n * L.MAX_LEGAL, dtype=torch.int32, device=dev)
+        self.mask_words = torch.zeros((self.n, L.MASK_WORDS), dtype=torch.int32, device=dev)
+
+    # ------------------------------------------------------------ lifetime
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib.jq_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    @staticmethod
+    def _ptr(t: torch.Tensor | None) -> int | None:
+        return None if t is None else t.data_ptr()
+
+    # ------------------------------------------------------------ reset
+    def upload_setup_pool(self, pool: np.ndarray) -> None:
+        pool = np.ascontiguousarray(pool, dtype=np.int8).reshape(-1, 120)
+        check(lib.jq_upload_setup_pool(self._h, pool.ctypes.data, pool.shape[0]))
+        self.pool = pool
+
+    def reset(self, seed_base: int = 0) -> None:
+        check(lib.jq_reset_seeded(self._h, int(seed_base), self.stream))
+
+    def reset_lineups(self, lineups: np.ndarray) -> None:
+        lu = np.ascontiguousarray(lineups, dtype=np.int8).reshape(self.n, 120)
+        check(lib.jq_reset_lineups(self._h, lu.ctypes.data, self.stream))
+
+    def reset_terminated(self, seed: int) -> None:
+        check(lib.jq_reset_terminated(self._h, int(seed), self.stream))
+
+    # ------------------------------------------------------------ step
+    def step(self, actions: torch.Tensor, acting: torch.Tensor | None = None, *,
+             canonical: bool = False) -> dict[str, torch.Tensor]:
+        a = actions.to(device=self.device, dtype=torch.int32).contiguous()
+        if a.shape != (self.n,):
+            raise ValueError(f"actions: expected ({self.n},), got {tuple(a.shape)}")
+        s = None
+        if acting is not None:
+            s = acting.to(device=self.device, dtype=torch.int8).contiguous()
+            if s.shape != (self.n,):
+                raise ValueError(f"acting: expected ({self.n},), got {tuple(s.shape)}")
+        if canonical and s is None:
+            raise ValueError("canonical actions need the acting seats")
+        dev, n = self.device, self.n
+        out = {
+            "valid": torch.empty(n, dtype=torch.bool, device=dev),
+            "event": torch.empty(n, dtype=torch.int8, device=dev),
+            "terminated": torch.empty(n, dtype=torch.bool, device=dev),
+            "winner_team": torch.empty(n, dtype=torch.int8, device=dev),
+            "draw": torch.empty(n, dtype=torch.bool, device=dev),
+            "flag_captured": torch.empty(n, dtype=torch.bool, device=dev),
+            "seats_died": torch.empty(n, dtype=torch.uint8, device=dev),
+            "rewards": torch.empty(n, dtype=torch.float32, device=dev),
+            "world_action": torch.empty(n, dtype=torch.int32, device=dev),
+        }
+        p = self._ptr
+        check(lib.jq_step(self._h, a.data_ptr(), p(s), L.ACT_CANONICAL if canonical else L.ACT_WORLD,
+                          p(out["valid"]), p(out["event"]), p(out["terminated"]), p(out["winner_team"]),
+                          p(out["draw"]), p(out["flag_captured"]), p(out["seats_died"]), p(out["rewards"]),
+                          p(out["world_action"]), self.stream))
+        return out
+
+    # ------------------------------------------------------------ legal actions
+    def legal(self, acting: torch.Tensor | None = None, *, csr: bool = True, mask_words: bool = True,
+              mask_bool: bool = False) -> dict[str, torch.Tensor]:
+        s = None if acting is None else acting.to(device=self.device, dtype=torch.int8).contiguous()
+        mb = torch.empty((self.n, L.ACTION_DIM), dtype=torch.bool, device=self.device) if mask_bool else None
+        p = self._ptr
+        check(lib.jq_legal(self._h, p(s), self.counts.data_ptr(),
+                           self.offsets.data_ptr() if csr else None, self.values.data_ptr() if csr else None,
+                           self.mask_words.data_ptr() if mask_words else None, p(mb), self.stream))
+        out = {"counts": self.counts}
+        if csr:
+            out["offsets"] = self.offsets
+            out["values"] = self.values
+        if mask_words:
+            out["mask_words"] = self.mask_words
+        if mask_bool:
+            out["mask_bool"] = mb
+        return out
+
+    def legal_csr_numpy(self, acting: torch.Tensor | None = None) -> tuple[np.ndarray, np.ndarray]:
+        self.legal(acting, csr=True, mask_words=False)
+        offsets = self.offsets.cpu().numpy()
+        values = self.values[: int(offsets[-1])].cpu().numpy()
+        return offsets, values
+
+    # ------------------------------------------------------------ observations
+    def observe(self, observer: torch.Tensor | None = None, *, fmt: str = "f32", all_seats: bool = False,
+                out_spatial: torch.Tensor | None = None, out_global: torch.Tensor | None = None,
+                out_aux: torch.Tensor | None = None):
+        code = {"f32": L.OBS_F32, "bf16": L.OBS_BF16, "u8": L.OBS_U8}[fmt]
+        dt = {"f32": torch.float32, "bf16": torch.bfloat16, "u8": torch.uint8}[fmt]
+        lead = (self.n, 4) if all_seats else (self.n,)
+        if out_spatial is None:
+            out_spatial = torch.empty(lead + (L.OBS_CHANNELS, 17, 17), dtype=dt, device=self.device)
+        if out_global is None:
+            out_global = torch.empty(lead + (L.OBS_GLOBALS,), dtype=torch.float32, device=self.device)
+        if fmt == "u8" and out_aux is None:
+            out_aux = torch.empty(lead + (L.AUX_PLANES, 17, 17), dtype=torch.float32, device=self.device)
+        if tuple(out_spatial.shape) != lead + (L.OBS_CHANNELS, 17, 17) or out_spatial.dtype != dt:
+            raise ValueError("out_spatial has the wrong shape or dtype")
+        s = None if observer is None else observer.to(device=self.device, dtype=torch.int8).contiguous()
+        check(lib.jq_observe(self._h, self._ptr(s), code, 1 if all_seats else 0, out_spatial.data_ptr(),
+                             self._ptr(out_aux) if fmt == "u8" else None, out_global.data_ptr(), self.stream))
+        if fmt == "u8":
+            return out_spatial, out_global, out_aux
+        return out_spatial, out_global
+
+    # ------------------------------------------------------------ sampling / fused step
+    def sample_uniform(self, seed: int, ply: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        if out is None:
+            out = torch.empty(self.n, dtype=torch.int32, device=self.device)
+        check(lib.jq_sample_uniform(self._h, self.counts.data_ptr(), self.offsets.data_ptr(),
+                                    self.values.data_ptr(), int(seed), int(ply), out.data_ptr(), self.stream))
+        return out
+
+    def env_step(self, *, actions: torch.Tensor | None = None, sample_seed: int = 0, ply: int = 0,
+                 reset_seed: int = 0, obs_fmt: str = "u8", spatial: torch.Tensor | None = None,
+                 aux: torch.Tensor | None = None, glob: torch.Tensor | None = None,
+                 terminated: torch.Tensor | None = None, reward: torch.Tensor | None = None,
+                 actions_out: torch.Tensor | None = None) -> None:
+        code = {"f32": L.OBS_F32, "bf16": L.OBS_BF16, "u8": L.OBS_U8}[obs_fmt]
+        p = self._ptr
+        check(lib.jq_env_step(self._h, p(actions), int(sample_seed), int(ply), int(reset_seed),
+                              self.counts.data_ptr(), self.offsets.data_ptr(), self.values.data_ptr(),
+                              self.mask_words.data_ptr(), code, p(spatial), p(aux), p(glob), p(terminated),
+                              p(reward), p(actions_out), self.stream))
+
+    # ------------------------------------------------------------ state import / export
+    def get_field(self, name: str) -> np.ndarray:
+        e, b = L.field_info(name)
+        kind = _FIELD_KIND.get(name, "i")
+        dt = np.dtype(_TYPESTR[(b, kind)])
+        out = np.zeros((self.n, e), dtype=dt)
+        check(lib.jq_get_field(self._h, L.FIELDS[name], out.ctypes.data))
+        return out
+
+    def set_field(self, name: str, arr: np.ndarray) -> None:
+        e, b = L.field_info(name)
+        kind = _FIELD_KIND.get(name, "i")
+        dt = np.dtype(_TYPESTR[(b, kind)])
+        a = np.ascontiguousarray(np.asarray(arr).astype(dt, copy=False).reshape(self.n, e))
+        check(lib.jq_set_field(self._h, L.FIELDS[name], a.ctypes.data))
+
+    def finalize_import(self) -> None:
+        check(lib.jq_finalize_import(self._h, self.stream))
+
+    def field_tensor(self, name: str, torch_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """Zero-copy device view of a per-env state field, shape (N, elems) or (N,)."""
+        e, b = L.field_info(name)
+        ptr = C.c_void_p()
+        check(lib.jq_field_ptr(self._h, L.FIELDS[name], C.byref(ptr)))
+        kind = _FIELD_KIND.get(name, "i")
+        ts = _TYPESTR[(b, kind)]
+        if torch_dtype is torch.bool:
+            ts = "|b1"
+        shape = (self.n,) if e == 1 else (self.n, e)
+        return torch.as_tensor(_CudaArrayView(ptr.value, shape, ts), device=self.device)
+
+    def sync(self) -> None:
+        torch.cuda.synchronize(self.device)

@@ -1,0 +1,905 @@
+// HIP kernels for the batched Junqi environment (gfx950, wave64); included by jq_lib.hip.
+//
+// Execution model: one wavefront owns one env. Its cell map and piece rows are
+// staged in LDS; rules logic that is serial by nature (one ply) runs uniformly on
+// all 64 lanes, and the wide parts are spread over lanes: the 30 pieces of a seat
+// for move generation, the 73 rail nodes for the engineer's reachability closure
+// (two 64-bit ballots per hop), the 120 pids for purges and Zobrist folds, and the
+// four observers for combat memory and beliefs.
+//
+// Reference semantics: junqi_core/state.py::GameState.step_inplace (638-998),
+// move_gen.py (SoA generator 1052-1199, legacy predicates 127-376),
+// combat_memory.py (339-569), info_model.py (218-429).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/junqi_amd.h"
+#include "jq_device.h"
+#include "jq_topology.h"
+
+namespace jq {
+
+__constant__ Tables cT;
+__constant__ uint8_t cBVAL[BC_COUNT][12];   // belief code x type -> obs value code
+__constant__ float cDECODE[256];             // obs value code -> float
+constexpr int JQ_MASK_WORDS_PAD = 528;
+
+// ------------------------------------------------------------------ helpers
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ uint16_t cflags(int f) { return cT.cflags[f]; }
+__device__ __forceinline__ bool is_on(int f) { return cflags(f) & CF_ON; }
+__device__ __forceinline__ bool is_rail(int f) { return cflags(f) & CF_RAIL; }
+__device__ __forceinline__ bool is_camp(int f) { return cflags(f) & CF_CAMP; }
+__device__ __forceinline__ bool is_sh(int f) { return cflags(f) & CF_SH; }
+__device__ __forceinline__ int curve_of(int f) { return cflags(f) >> 8; }
+__device__ __forceinline__ int team_of(int pid) { return (pid / 30) & 1; }
+
+__device__ __forceinline__ bool enemy_att(const int8_t *cell, int f, int team)
+{   // enemy piece on a non-camp cell (move_gen.py:822-867)
+    const int p = cell[f];
+    return p >= 0 && team_of(p) != team && !is_camp(f);
+}
+__device__ __forceinline__ bool landable(const int8_t *cell, int f, int team)
+{
+    return cell[f] < 0 || enemy_att(cell, f, team);
+}
+
+__device__ __forceinline__ void setbit3(uint64_t &m0, uint64_t &m1, uint64_t &m2, int c)
+{
+    const uint64_t b = 1ull << (c & 63);
+    const int w = c >> 6;
+    m0 |= (w == 0) ? b : 0ull;
+    m1 |= (w == 1) ? b : 0ull;
+    m2 |= (w == 2) ? b : 0ull;
+}
+
+__device__ __forceinline__ uint64_t wave_or(uint64_t v)
+{
+    for (int o = 32; o > 0; o >>= 1) v |= (uint64_t)__shfl_xor((long long)v, o);
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_xor(uint64_t v)
+{
+    for (int o = 32; o > 0; o >>= 1) v ^= (uint64_t)__shfl_xor((long long)v, o);
+    return v;
+}
+__device__ __forceinline__ int wave_sum(int v)
+{
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Reachability closure of an engineer standing on rail index `src_r`: the source
+// plus every rail node joined to it through empty rail cells. Lane l evaluates
+// nodes l and l+64 each hop; the frontier grows until a hop adds nothing.
+__device__ void rail_closure(const int8_t *cell, int src_r, uint64_t &r0, uint64_t &r1)
+{
+    const int l = lane_id();
+    const int v1 = l + 64;
+    const bool e0 = cell[cT.railcell[l]] < 0;
+    const bool e1 = v1 < NRAIL && cell[cT.railcell[v1 < NRAIL ? v1 : 0]] < 0;
+    const uint64_t a0 = cT.rnbr[l][0], a1 = cT.rnbr[l][1];
+    const uint64_t b0 = v1 < NRAIL ? cT.rnbr[v1][0] : 0ull, b1 = v1 < NRAIL ? cT.rnbr[v1][1] : 0ull;
+    r0 = src_r < 64 ? (1ull << src_r) : 0ull;
+    r1 = src_r >= 64 ? (1ull << (src_r - 64)) : 0ull;
+    for (int hop = 0; hop < NRAIL; ++hop) {
+        const bool n0 = e0 && !((r0 >> l) & 1) && (((a0 & r0) | (a1 & r1)) != 0);
+        const bool n1 = e1 && !((r1 >> (v1 & 63)) & 1) && (((b0 & r0) | (b1 & r1)) != 0);
+        const uint64_t g0 = __ballot(n0), g1 = __ballot(n1);
+        if (!(g0 | g1)) break;
+        r0 |= g0;
+        r1 |= g1 & 0x1FFull;
+    }
+}
+
+// Engineer destinations (move_gen.py:870-895) as a compact-index mask (uniform).
+__device__ void engineer_mask(const int8_t *cell, int src, int team, uint64_t &m0, uint64_t &m1, uint64_t &m2)
+{
+    const int l = lane_id();
+    const int sr = cT.railidx[src];
+    uint64_t r0, r1;
+    rail_closure(cell, sr, r0, r1);
+    uint64_t p0 = 0, p1 = 0, p2 = 0;
+    for (int v = l; v < NRAIL; v += 64) {
+        const bool adj = ((cT.rnbr[v][0] & r0) | (cT.rnbr[v][1] & r1)) != 0;
+        const int f = cT.railcell[v];
+        if (v != sr && adj && landable(cell, f, team)) setbit3(p0, p1, p2, cT.f2c[f]);
+    }
+    m0 = wave_or(p0); m1 = wave_or(p1); m2 = wave_or(p2);
+}
+
+// Road steps and (for non-engineers) straight rays and curve runs of one piece,
+// computed by the calling lane alone (move_gen.py:1052-1199 parts a, b, c, e).
+__device__ void piece_mask_lane(const int8_t *cell, int src, int team, bool engineer,
+                                uint64_t &m0, uint64_t &m1, uint64_t &m2)
+{
+    m0 = m1 = m2 = 0;
+    for (int k = 0; k < 4; ++k) {
+        const int nb = cT.adj[src][k];
+        if (nb >= 0 && landable(cell, nb, team)) setbit3(m0, m1, m2, cT.f2c[nb]);
+    }
+    for (int k = 0; k < 4; ++k) {
+        const int nb = cT.diag[src][k];
+        if (nb >= 0 && landable(cell, nb, team)) setbit3(m0, m1, m2, cT.f2c[nb]);
+    }
+    if (engineer) return;
+    const int r = cT.railidx[src];
+    if (r < 0) return;
+    for (int k = 0; k < 4; ++k) {
+        const int len = cT.raylen[r][k];
+        for (int i = 0; i < len; ++i) {
+            const int nb = cT.rays[r][k][i];
+            if (cell[nb] < 0) { setbit3(m0, m1, m2, cT.f2c[nb]); continue; }
+            if (enemy_att(cell, nb, team)) setbit3(m0, m1, m2, cT.f2c[nb]);
+            break;
+        }
+    }
+    for (int d = 0; d < 2; ++d) {
+        const int len = cT.craylen[r][d];
+        for (int i = 0; i < len; ++i) {
+            const int nb = cT.crays[r][d][i];
+            if (cell[nb] < 0) { setbit3(m0, m1, m2, cT.f2c[nb]); continue; }
+            if (enemy_att(cell, nb, team)) setbit3(m0, m1, m2, cT.f2c[nb]);
+            break;
+        }
+    }
+}
+
+// dst on a straight run (k < 4) or curve run of src with every earlier cell empty
+// (move_gen.py:127-171 and 384-423).
+__device__ bool run_clear(const int8_t *cell, int src, int dst, bool curve)
+{
+    const int r = cT.railidx[src];
+    if (r < 0) return false;
+    const int nruns = curve ? 2 : 4;
+    for (int k = 0; k < nruns; ++k) {
+        const int len = curve ? cT.craylen[r][k] : cT.raylen[r][k];
+        for (int i = 0; i < len; ++i) {
+            const int nb = curve ? cT.crays[r][k][i] : cT.rays[r][k][i];
+            if (nb == dst) return true;
+            if (cell[nb] >= 0) break;
+        }
+    }
+    return false;
+}
+
+__device__ bool engineer_reaches(const int8_t *cell, int src, int dst)
+{   // move_gen.py:186-224
+    if (!is_rail(src) || !is_rail(dst) || src == dst) return false;
+    uint64_t r0, r1;
+    rail_closure(cell, cT.railidx[src], r0, r1);
+    const int dr = cT.railidx[dst];
+    return ((cT.rnbr[dr][0] & r0) | (cT.rnbr[dr][1] & r1)) != 0;
+}
+
+// is_legal_move (move_gen.py:299-376), uniform over the wave.
+__device__ bool legal_pair(const int8_t *cell, const int8_t *ptype, int seat, int src, int dst)
+{
+    if (src < 0 || src >= NC || dst < 0 || dst >= NC || src == dst) return false;
+    if (!is_on(src) || !is_on(dst)) return false;
+    const int p = cell[src];
+    if (p < 0 || p / 30 != seat) return false;
+    const int t = ptype[p];
+    if (t < T_ZHADAN || t > T_GONGB) return false;   // JUNQI / DILEI never move (no other value is a piece)
+    if (is_sh(src)) return false;
+    if (!landable(cell, dst, seat & 1)) return false;
+    const int sx = src % 17, sy = src / 17, dx = dst % 17, dy = dst / 17;
+    const int adx = abs(sx - dx), ady = abs(sy - dy);
+    if (adx <= 1 && ady <= 1) {
+        if (adx == 1 && ady == 1) { if (is_camp(src) || is_camp(dst)) return true; }
+        else return true;
+    }
+    if (!(is_rail(src) && is_rail(dst))) return false;
+    if (t == T_GONGB) return engineer_reaches(cell, src, dst);
+    if (sx == dx || sy == dy) return run_clear(cell, src, dst, false);
+    if (curve_of(src) > 0 && curve_of(src) == curve_of(dst)) return run_clear(cell, src, dst, true);
+    return false;
+}
+
+// move_requires_gongb (move_gen.py:245-296) for a legal engineer move.
+__device__ bool engineer_only(const int8_t *cell, int src, int dst)
+{
+    const int sx = src % 17, sy = src / 17, dx = dst % 17, dy = dst / 17;
+    const int adx = abs(sx - dx), ady = abs(sy - dy);
+    if (adx + ady == 1) return false;
+    if (adx == 1 && ady == 1 && (is_camp(src) || is_camp(dst))) return false;
+    if (!(is_rail(src) && is_rail(dst))) return false;
+    if (sx == dx || sy == dy) {
+        if (run_clear(cell, src, dst, false)) return false;
+        return engineer_reaches(cell, src, dst);
+    }
+    if (curve_of(src) > 0 && curve_of(src) == curve_of(dst) && run_clear(cell, src, dst, true)) return false;
+    return engineer_reaches(cell, src, dst);
+}
+
+// Does `seat` have a legal move (the Q12 test, state.py:1139-1165)?
+__device__ bool seat_has_move(const int8_t *cell, const int16_t *pos, const int8_t *ptype, int seat)
+{
+    const int l = lane_id(), team = seat & 1;
+    bool mov = false, quick = false, eng = false;
+    int src = -1;
+    if (l < 30) {
+        const int pid = seat * 30 + l;
+        src = pos[pid];
+        const int t = ptype[pid];
+        mov = src >= 0 && t != T_JUNQI && t != T_DILEI && !is_sh(src);
+        if (mov) {
+            eng = t == T_GONGB;
+            for (int k = 0; k < 4; ++k) { const int nb = cT.adj[src][k]; quick |= nb >= 0 && cell[nb] < 0; }
+        }
+    }
+    if (__ballot(mov && quick)) return true;
+    uint64_t m0 = 0, m1 = 0, m2 = 0;
+    if (mov) piece_mask_lane(cell, src, team, eng, m0, m1, m2);
+    if (__ballot((m0 | m1 | m2) != 0)) return true;
+    uint64_t engs = __ballot(mov && eng && is_rail(src < 0 ? 0 : src));
+    while (engs) {
+        const int e = __builtin_ctzll(engs);
+        engs &= engs - 1;
+        const int esrc = __shfl(src, e);
+        uint64_t e0, e1, e2;
+        engineer_mask(cell, esrc, team, e0, e1, e2);
+        if (e0 | e1 | e2) return true;
+    }
+    return false;
+}
+
+__device__ __forceinline__ int resolve_combat(int a, int d)
+{   // rules.py:466-516, rows in order
+    if (a == T_ZHADAN || d == T_ZHADAN) return EV_BOMB;
+    if (d == T_JUNQI) return EV_EAT;
+    if (d == T_DILEI) return a == T_GONGB ? EV_EAT : EV_KILLED;
+    if (a == d) return EV_BOMB;
+    return a < d ? EV_EAT : EV_KILLED;
+}
+
+__device__ __forceinline__ uint64_t zp(const uint64_t *z, int pid, int t, int f)
+{   // indexes come from state rows; out-of-range values read entry 0 instead of faulting
+    pid = (unsigned)pid < 120u ? pid : 0;
+    t = (unsigned)t < 14u ? t : 0;
+    f = (unsigned)f < 289u ? f : 0;
+    return z[((size_t)pid * 14 + t) * 289 + f];
+}
+
+__device__ __forceinline__ int tracked(int t) { return (t >= 2 && t <= 13) ? t - 2 : -1; }
+__device__ __forceinline__ bool code_onehot(int c) { return c >= 1 && c <= 12; }
+__device__ __forceinline__ int rank_floor_next(int t)
+{   // combat_memory.py:163-173: ordinary rank GONGB=1..SILING=9, floor = min(rank+1, 9)
+    if (t < T_SILING || t > T_GONGB) return 0;
+    const int r = T_GONGB - t + 1;
+    return r + 1 < 9 ? r + 1 : 9;
+}
+__device__ __forceinline__ bool sees_truth(int o, int owner, int mode)
+{   // info_model.py:568-577
+    if (mode == SM_BRIGHT || o == owner) return true;
+    return mode == SM_HALF_DARK && ((o & 1) == (owner & 1));
+}
+
+// ------------------------------------------------------------------ step
+struct StepOut {
+    uint8_t *valid; int8_t *event; uint8_t *term; int8_t *winner; uint8_t *draw;
+    uint8_t *fcap; uint8_t *died; float *reward; int32_t *world;
+};
+
+// Kill pid at its current cell (state.py:1027-1049). Uniform; lane 0 stores.
+__device__ void kill_piece(const State &S, int env, int8_t *cell, int16_t *pos, const int8_t *ptype, int pid,
+                           int reason, int loc, int step, uint64_t &zob)
+{
+    const int cur = pos[pid];
+    if ((unsigned)cur >= (unsigned)NC) return;
+    zob ^= zp(S.ztab, pid, ptype[pid], cur);
+    __syncthreads();
+    if (lane_id() == 0) {
+        cell[cur] = -1; pos[pid] = -1;
+        const size_t pi = (size_t)env * PID_STRIDE + pid;
+        S.pos[pi] = -1; S.dreason[pi] = (int8_t)reason; S.dstep[pi] = (int16_t)step; S.dloc[pi] = (int16_t)loc;
+        S.cell[(size_t)env * CELL_STRIDE + cur] = -1;
+    }
+    __syncthreads();
+}
+
+__device__ void move_piece(const State &S, int env, int8_t *cell, int16_t *pos, const int8_t *ptype, int pid,
+                           int src, int dst, uint64_t &zob)
+{   // state.py:1005-1025
+    const int t = ptype[pid];
+    zob ^= zp(S.ztab, pid, t, src) ^ zp(S.ztab, pid, t, dst);
+    __syncthreads();
+    if (lane_id() == 0) {
+        cell[src] = -1; cell[dst] = (int8_t)pid; pos[pid] = (int16_t)dst;
+        S.cell[(size_t)env * CELL_STRIDE + src] = -1;
+        S.cell[(size_t)env * CELL_STRIDE + dst] = (int8_t)pid;
+        S.pos[(size_t)env * PID_STRIDE + pid] = (int16_t)dst;
+    }
+    __syncthreads();
+}
+
+// Remove every live piece of `seat` (state.py:1639-1692): KILLED_BY_ENEMY at the
+// piece's current cell. Lanes 0..29 take one pid each; Zobrist folded by XOR.
+__device__ void purge_seat(const State &S, int env, int8_t *cell, int16_t *pos, const int8_t *ptype, int seat,
+                           int step, uint64_t &zob)
+{
+    const int l = lane_id();
+    uint64_t z = 0;
+    __syncthreads();
+    if (l < 30) {
+        const int pid = seat * 30 + l;
+        const int cur = pos[pid];
+        if ((unsigned)cur < (unsigned)NC) {
+            z = zp(S.ztab, pid, ptype[pid], cur);
+            cell[cur] = -1; pos[pid] = -1;
+            const size_t pi = (size_t)env * PID_STRIDE + pid;
+            S.pos[pi] = -1; S.dreason[pi] = 0; S.dstep[pi] = (int16_t)step; S.dloc[pi] = (int16_t)cur;
+            S.cell[(size_t)env * CELL_STRIDE + cur] = -1;
+        }
+    }
+    zob ^= wave_xor(z);
+    __syncthreads();
+}
+
+// CombatMemory update for EAT / KILLED (combat_memory.py:354-569). Lane o < 4
+// handles observer o; observers never touch each other's rows.
+__device__ void cm_apply(const State &S, int env, bool is_eat, int apid, int dpid, int aseat, int dseat,
+                         int atype, int dtype, int step)
+{
+    const int o = lane_id();
+    if (o >= 4) return;
+    int K, V, Vs, Vt;
+    if (is_eat) { K = apid; V = dpid; Vs = dseat; Vt = dtype; }
+    else        { K = dpid; V = apid; Vs = aseat; Vt = atype; }
+    const size_t kI = cm_idx(env, o, K), vI = cm_idx(env, o, V);
+    uint8_t kflags = S.cm_flags[kI];
+    const uint8_t vflags = S.cm_flags[vI];
+    if (!is_eat) {
+        const bool known = (vflags & CMF_IS_GONGB) || (atype == T_GONGB && o == Vs);
+        if (known) kflags |= CMF_ATK_GONGB;
+    }
+    const uint64_t vdlo = S.cm_dlo[vI], vdhi = S.cm_dhi[vI], vclo = S.cm_clo[vI], vchi = S.cm_chi[vI];
+    uint64_t kclo = S.cm_clo[kI] | vdlo | vclo, kchi = S.cm_chi[kI] | vdhi | vchi;
+    if (V < 64) kclo |= 1ull << V; else kchi |= 1ull << (V - 64);
+    uint16_t kctype = (uint16_t)(S.cm_ctype[kI] | S.cm_dtype[vI] | S.cm_ctype[vI]);
+    int kfloor = S.cm_floor[kI];
+    int16_t kfstep = S.cm_fstep[kI];
+    const int vfloor = S.cm_floor[vI];
+    if (vfloor > 0) {
+        const int prop = vfloor + 1 < 9 ? vfloor + 1 : 9;
+        if (prop > kfloor) { kfloor = prop; kfstep = (int16_t)step; }
+        kflags |= CMF_NOT_GONGB;
+    }
+    // v6 reverse projection: observer's own pids V had eaten (directly or by chain),
+    // plus V itself when V belongs to the observer, are now eaten by K too.
+    {
+        uint64_t mlo = 0, mhi = 0;
+        const int b0 = o * 30;
+        for (int s = 0; s < 30; ++s) { const int gp = b0 + s; if (gp < 64) mlo |= 1ull << gp; else mhi |= 1ull << (gp - 64); }
+        uint64_t vlo = (vdlo | vclo) & mlo, vhi = (vdhi | vchi) & mhi;
+        if (Vs == o) { if (V < 64) vlo |= 1ull << V; else vhi |= 1ull << (V - 64); }
+        const uint64_t klo = K < 64 ? (1ull << K) : 0ull, khi = K >= 64 ? (1ull << (K - 64)) : 0ull;
+        while (vlo) { const int b = __builtin_ctzll(vlo); vlo &= vlo - 1; const size_t t = cm_idx(env, o, b); S.cm_elo[t] |= klo; S.cm_ehi[t] |= khi; }
+        while (vhi) { const int b = __builtin_ctzll(vhi) + 64; vhi &= vhi - 1; const size_t t = cm_idx(env, o, b); S.cm_elo[t] |= klo; S.cm_ehi[t] |= khi; }
+    }
+    int16_t kldir = S.cm_ldir[kI];
+    if (Vs != o) {
+        const int c = S.cm_ocnt[kI] + 1;
+        S.cm_ocnt[kI] = (int16_t)(c < 32767 ? c : 32767);
+        kldir = (int16_t)step;
+    } else {
+        uint64_t kdlo = S.cm_dlo[kI], kdhi = S.cm_dhi[kI];
+        if (V < 64) kdlo |= 1ull << V; else kdhi |= 1ull << (V - 64);
+        S.cm_dlo[kI] = kdlo; S.cm_dhi[kI] = kdhi;
+        const int vi = tracked(Vt);
+        if (vi >= 0) {
+            S.cm_dtype[kI] = (uint16_t)(S.cm_dtype[kI] | (1u << vi));
+            kctype |= (uint16_t)(1u << vi);
+        }
+        kldir = (int16_t)step;
+        if (is_eat) kflags |= (Vt == T_DILEI) ? CMF_IS_GONGB : CMF_NOT_GONGB;
+        if (Vt >= T_SILING && Vt <= T_GONGB) {
+            const int pr = rank_floor_next(Vt);
+            if (pr > kfloor) { kfloor = pr; kfstep = (int16_t)step; }
+        }
+    }
+    S.cm_clo[kI] = kclo; S.cm_chi[kI] = kchi; S.cm_ctype[kI] = kctype;
+    S.cm_lchain[kI] = (int16_t)step; S.cm_ldir[kI] = kldir;
+    S.cm_floor[kI] = (int8_t)kfloor; S.cm_fstep[kI] = kfstep; S.cm_flags[kI] = kflags;
+}
+
+// BeliefTensor.update for the four observers (info_model.py:271-429). Entries are
+// keyed by pid so R1 migration is implicit; lane o < 4 handles observer o.
+__device__ void belief_update(const State &S, int env, const int8_t *cell, int sp, int dp, int ss, int ds,
+                              int dt, int dst, int ev, bool rsrc, bool rdst, bool fcap, int died)
+{
+    const int o = lane_id();
+    if (o >= 4) return;
+    uint8_t *bc = S.bcode + ((size_t)env * 4 + o) * PID_STRIDE;
+    int8_t *rem = S.rem + ((size_t)env * 4 + o) * 48;
+    uint8_t trk = S.remtrk[(size_t)env * 4 + o];
+    auto dec = [&](int seat, int ti) {
+        if ((trk >> seat) & 1) { int8_t &c = rem[seat * 12 + ti]; if (c > 0) --c; }
+    };
+    int acode = bc[sp];
+    const int dcode = dp >= 0 ? bc[dp] : 0;
+    if (rsrc) dec(ss, T_SILING - 2);
+    if (rdst) dec(ds, T_SILING - 2);
+    if (ev == EV_EAT && dp >= 0 && dt == T_DILEI && !code_onehot(acode)) {
+        acode = 1 + (T_GONGB - 2);
+        bc[sp] = (uint8_t)acode;
+        dec(ss, T_GONGB - 2);
+    }
+    if (fcap) {
+        trk &= (uint8_t)~(1u << ds);
+    } else if (ev == EV_EAT && dp >= 0 && is_sh(dst) && cT.owner[dst] == ds) {
+        const int other = cT.sh_other[dst];
+        const int op = cell[other];
+        if (op >= 0 && !code_onehot(bc[op])) bc[op] = (uint8_t)(1 + (T_JUNQI - 2));
+    }
+    auto removed = [&](int seat, int code) { if (((trk >> seat) & 1) && code_onehot(code)) dec(seat, code - 1); };
+    if (ev == EV_EAT) { if (dp >= 0) removed(ds, dcode); }
+    else if (ev == EV_KILLED) removed(ss, acode);
+    else if (ev == EV_BOMB) { removed(ss, acode); if (dp >= 0) removed(ds, dcode); }
+    trk &= (uint8_t)~died;
+    S.remtrk[(size_t)env * 4 + o] = trk;
+}
+
+__global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict__ actions,
+                                             const int8_t *__restrict__ acting, int act_fmt, StepOut O)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    __shared__ int8_t cell[CELL_STRIDE];
+    __shared__ int16_t pos[PID_STRIDE];
+    __shared__ int8_t ptype[PID_STRIDE];
+
+    const bool was_term = S.term[env] != 0;
+    const int seat = S.turn[env];
+    if (l == 0) {
+        if (O.valid) O.valid[env] = 0;
+        if (O.event) O.event[env] = 0;
+        if (O.term) O.term[env] = was_term;
+        if (O.winner) O.winner[env] = S.winner[env];
+        if (O.draw) O.draw[env] = S.draw[env];
+        if (O.fcap) O.fcap[env] = 0;
+        if (O.died) O.died[env] = 0;
+        if (O.reward) O.reward[env] = 0.f;
+        if (O.world) O.world[env] = -1;
+    }
+    if (was_term) return;
+
+    const int32_t a = actions[env];
+    int src = -1, dst = -1;
+    if (act_fmt == 1) {
+        const int as = acting ? acting[env] : seat;
+        if (a >= 0 && a < NONB * NONB && as >= 0 && as < 4) {
+            src = cT.unrot[as][cT.c2f[a / NONB]];
+            dst = cT.unrot[as][cT.c2f[a % NONB]];
+        }
+    } else if (a >= 0 && a < NC * NC) {
+        src = a / NC; dst = a % NC;
+    }
+    if (l == 0 && O.world && src >= 0) O.world[env] = src * NC + dst;
+    if (src < 0) return;
+    if (acting && acting[env] != seat) return;
+    const uint8_t sdead0 = S.sdead[env];
+    if ((sdead0 >> seat) & 1) return;
+
+    for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
+    for (int p = l; p < PID_STRIDE; p += 64) {
+        pos[p] = S.pos[(size_t)env * PID_STRIDE + p];
+        ptype[p] = S.ptype[(size_t)env * PID_STRIDE + p];
+    }
+    __syncthreads();
+    if (!legal_pair(cell, ptype, seat, src, dst)) return;
+
+    const int mc0 = S.mc[env], mslc0 = S.mslc[env];
+    uint64_t zob = S.zob[env];
+    const uint64_t *Z = S.ztab;
+    zob ^= Z[ZOFF_TURN + seat] ^ Z[ZOFF_MC + (mc0 & 0xFFF)] ^ Z[ZOFF_MSLC + (mslc0 & 0x1FF)];
+    const int step = mc0 + 1;
+    int died = 0;
+    uint8_t sdead = sdead0, sflag = S.sflag[env];
+    const int sp = cell[src], dp = cell[dst];
+    const int st = ptype[sp], dt = dp >= 0 ? ptype[dp] : -1;
+    const int ss = sp / 30, ds = dp >= 0 ? dp / 30 : -1;
+
+    if (st == T_GONGB && engineer_only(cell, src, dst)) {
+        if (l < 4) S.cm_flags[cm_idx(env, l, sp)] |= CMF_IS_GONGB;
+    }
+    // move history (state.py:673-678)
+    if (l == 0) {
+        const int meta = S.hmeta[env];
+        const int cnt = meta & 0xFF, head = (meta >> 8) & 31;
+        S.hist[(size_t)env * HIST_LEN + head] = src | (dst << 16);
+        S.hmeta[env] = (cnt < 32 ? cnt + 1 : 32) | (((head + 1) & 31) << 8);
+    }
+    int ev;
+    bool rsrc = false, rdst = false, fcap = false;
+    auto set_flag = [&](int s) { if (!((sflag >> s) & 1)) { sflag |= (uint8_t)(1u << s); zob ^= Z[ZOFF_SFLAG + s]; } };
+    auto set_dead = [&](int s) { if (!((sdead >> s) & 1)) { sdead |= (uint8_t)(1u << s); zob ^= Z[ZOFF_SDEAD + s]; } };
+    if (dp < 0) {
+        ev = EV_MOVE;
+        if (l == 0) S.mcount[(size_t)env * PID_STRIDE + sp] += 1;
+        move_piece(S, env, cell, pos, ptype, sp, src, dst, zob);
+    } else {
+        ev = resolve_combat(st, dt);
+        rsrc = st == T_SILING && (ev == EV_KILLED || ev == EV_BOMB);
+        rdst = dt == T_SILING && (ev == EV_EAT || ev == EV_BOMB);
+        fcap = dt == T_JUNQI;
+        if (rsrc) set_flag(ss);
+        if (rdst) set_flag(ds);
+        if (ev == EV_EAT) {
+            if (l == 0) S.aeat[(size_t)env * PID_STRIDE + sp] += 1;
+            kill_piece(S, env, cell, pos, ptype, dp, 0, dst, step, zob);
+            move_piece(S, env, cell, pos, ptype, sp, src, dst, zob);
+            cm_apply(S, env, true, sp, dp, ss, ds, st, dt, step);
+        } else if (ev == EV_KILLED) {
+            if (l == 0) S.psurv[(size_t)env * PID_STRIDE + dp] += 1;
+            kill_piece(S, env, cell, pos, ptype, sp, (dt == T_DILEI || dt == T_ZHADAN) ? 1 : 0, dst, step, zob);
+            cm_apply(S, env, false, sp, dp, ss, ds, st, dt, step);
+        } else {
+            kill_piece(S, env, cell, pos, ptype, sp, 2, dst, step, zob);
+            kill_piece(S, env, cell, pos, ptype, dp, 2, dst, step, zob);
+        }
+    }
+    if (fcap && !((sdead >> ds) & 1)) {   // state.py:864-890
+        set_dead(ds); set_flag(ds);
+        purge_seat(S, env, cell, pos, ptype, ds, step, zob);
+        died |= 1 << ds;
+    }
+    {   // dead sweep (state.py:895-901)
+        const int p0 = l, p1 = l + 64;
+        const bool a0 = pos[p0] >= 0, a1 = p1 < NP && pos[p1] >= 0;
+        for (int s = 0; s < 4; ++s) {
+            const bool has = __ballot((a0 && p0 / 30 == s) || (a1 && p1 / 30 == s)) != 0;
+            if (!((sdead >> s) & 1) && !has) { set_dead(s); died |= 1 << s; }
+        }
+    }
+    const int nmc = mc0 + 1, nmslc = ev == EV_MOVE ? mslc0 + 1 : 0;
+    auto victory = [&](int &term, int &win, int &drw) {   // state.py:1695-1726
+        const bool red = !(((sdead >> 0) & 1) && ((sdead >> 2) & 1));
+        const bool blue = !(((sdead >> 1) & 1) && ((sdead >> 3) & 1));
+        term = 0; win = -1; drw = 0;
+        if (!red && !blue) { term = 1; win = seat & 1; return; }
+        if (!red) { term = 1; win = 1; return; }
+        if (!blue) { term = 1; win = 0; return; }
+        if (nmc >= 4000 || nmslc >= 200) { term = 1; drw = 1; }
+    };
+    int term, win, drw, nturn;
+    victory(term, win, drw);
+    if (!term) {   // state.py:1109-1167
+        int cand = (seat + 1) & 3;
+        for (int it = 0; it < 4; ++it) {
+            if ((sdead >> cand) & 1) { cand = (cand + 1) & 3; continue; }
+            if (seat_has_move(cell, pos, ptype, cand)) break;
+            set_dead(cand);
+            purge_seat(S, env, cell, pos, ptype, cand, step, zob);
+            died |= 1 << cand;
+            cand = (cand + 1) & 3;
+        }
+        nturn = cand;
+        victory(term, win, drw);
+    } else {
+        nturn = seat;
+    }
+    if (!term && nmc >= S.max_moves) { term = 1; drw = 1; }   // env move cap
+    zob ^= Z[ZOFF_TURN + nturn] ^ Z[ZOFF_MC + (nmc & 0xFFF)] ^ Z[ZOFF_MSLC + (nmslc & 0x1FF)];
+    if (term) zob ^= Z[ZOFF_TERM];
+    if (drw) zob ^= Z[ZOFF_DRAW];
+    if (win >= 0) zob ^= Z[ZOFF_WIN] ^ Z[ZOFF_WIN + win + 1];
+
+    belief_update(S, env, cell, sp, dp, ss, ds, dt, dst, ev, rsrc, rdst, fcap, died);
+
+    if (l == 0) {
+        S.mc[env] = nmc; S.mslc[env] = nmslc; S.turn[env] = (int8_t)nturn;
+        S.term[env] = (uint8_t)term; S.winner[env] = (int8_t)win; S.draw[env] = (uint8_t)drw;
+        S.sdead[env] = sdead; S.sflag[env] = sflag; S.zob[env] = zob;
+        if (O.valid) O.valid[env] = 1;
+        if (O.event) O.event[env] = (int8_t)ev;
+        if (O.term) O.term[env] = (uint8_t)term;
+        if (O.winner) O.winner[env] = (int8_t)win;
+        if (O.draw) O.draw[env] = (uint8_t)drw;
+        if (O.fcap) O.fcap[env] = fcap;
+        if (O.died) O.died[env] = (uint8_t)died;
+        if (O.reward) O.reward[env] = (term && !drw && win >= 0) ? (((seat & 1) == win) ? 1.f : -1.f) : 0.f;
+    }
+}
+
+// ------------------------------------------------------------------ reset
+// Start an env from a lineup (GameState.new_game, state.py:490-620; beliefs,
+// info_model.py:218-265). Zobrist includes every term new_game XORs in.
+__device__ void init_env(const State &S, int env, const int8_t *types)
+{
+    const int l = lane_id();
+    int8_t *cell = S.cell + (size_t)env * CELL_STRIDE;
+    for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = -1;
+    __syncthreads();
+    uint64_t z = 0;
+    for (int p = l; p < PID_STRIDE; p += 64) {
+        const size_t pi = (size_t)env * PID_STRIDE + p;
+        const int t = p < NP ? types[p] : 0;
+        const bool alive = t != T_NONE && cT.home[p < NP ? p : 0] >= 0 && p < NP;
+        const int h = alive ? cT.home[p] : -1;
+        S.ptype[pi] = alive ? (int8_t)t : (int8_t)-1;
+        S.pos[pi] = (int16_t)h; S.zero[pi] = (int16_t)h;
+        S.mcount[pi] = 0; S.aeat[pi] = 0; S.psurv[pi] = 0;
+        S.dreason[pi] = -1; S.dstep[pi] = -1; S.dloc[pi] = -1;
+        if (alive) { cell[h] = (int8_t)p; z ^= zp(S.ztab, p, t, h); }
+        for (int o = 0; o < 4; ++o) {
+            uint8_t code = 0;
+            if (alive) code = sees_truth(o, p / 30, S.show_mode) ? (uint8_t)(1 + t - 2) : (uint8_t)(BC_PRIOR0 + p % 30);
+            S.bcode[((size_t)env * 4 + o) * PID_STRIDE + p] = code;
+            const size_t ci = cm_idx(env, o, p);
+            S.cm_dlo[ci] = 0; S.cm_dhi[ci] = 0; S.cm_clo[ci] = 0; S.cm_chi[ci] = 0;
+            S.cm_elo[ci] = 0; S.cm_ehi[ci] = 0; S.cm_dtype[ci] = 0; S.cm_ctype[ci] = 0;
+            S.cm_ldir[ci] = -1; S.cm_ocnt[ci] = 0; S.cm_lchain[ci] = -1; S.cm_fstep[ci] = -1;
+            S.cm_floor[ci] = 0; S.cm_flags[ci] = 0;
+        }
+    }
+    z = wave_xor(z);
+    static constexpr int8_t kCounts[12] = {1, 3, 2, 1, 1, 2, 2, 2, 2, 3, 3, 3};
+    for (int i = l; i < 4 * 48; i += 64) {
+        const int o = i / 48, s = (i / 12) % 4, t = i % 12;
+        const bool tracked_seat = s != o && ((s & 1) != (o & 1));
+        S.rem[(size_t)env * 4 * 48 + i] = tracked_seat ? kCounts[t] : 0;
+    }
+    if (l < 4) {
+        uint8_t trk = 0;
+        for (int s = 0; s < 4; ++s) if (s != l && ((s & 1) != (l & 1))) trk |= (uint8_t)(1u << s);
+        S.remtrk[(size_t)env * 4 + l] = trk;
+    }
+    if (l == 0) {
+        const uint64_t *Z = S.ztab;
+        z ^= Z[ZOFF_TURN + 0] ^ Z[ZOFF_MC + 0] ^ Z[ZOFF_MSLC + 0] ^ Z[ZOFF_WIN + 0] ^ Z[ZOFF_SHOW + S.show_mode];
+        S.zob[env] = z;
+        S.turn[env] = 0; S.term[env] = 0; S.winner[env] = -1; S.draw[env] = 0;
+        S.sdead[env] = 0; S.sflag[env] = 0; S.mc[env] = 0; S.mslc[env] = 0; S.hmeta[env] = 0;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_reset_lineups(State S, const int8_t *__restrict__ lineups)
+{
+    const int env = blockIdx.x;
+    if (env >= S.n) return;
+    init_env(S, env, lineups + (size_t)env * NP);
+}
+
+__global__ __launch_bounds__(64) void k_reset_terminated(State S, int64_t seed)
+{
+    const int env = blockIdx.x;
+    if (env >= S.n || !S.term[env]) return;
+    // pool pick of the reference reset kernel (game_state.cu:2986-2991)
+    uint64_t h = (uint64_t)env * 2654435761ull + (uint64_t)seed;
+    h ^= h >> 17;
+    h *= 0xbf58476d1ce4e5b9ull;
+    h ^= h >> 31;
+    const int idx = (int)(h % (uint64_t)S.pool_size);
+    init_env(S, env, S.pool + (size_t)idx * NP);
+}
+
+// Recompute Zobrist and re-seed beliefs from the current board (hand-built states).
+__global__ __launch_bounds__(64) void k_finalize(State S)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    uint64_t z = 0;
+    for (int p = l; p < NP; p += 64) {
+        const size_t pi = (size_t)env * PID_STRIDE + p;
+        const int f = S.pos[pi], t = S.ptype[pi];
+        if (f >= 0 && t >= 0) z ^= zp(S.ztab, p, t, f);
+        for (int o = 0; o < 4; ++o) {
+            uint8_t code = 0;
+            if (f >= 0 && t >= 2) {
+                if (sees_truth(o, p / 30, S.show_mode)) code = (uint8_t)(1 + t - 2);
+                else code = (cT.owner[f] == p / 30) ? (uint8_t)(BC_PRIOR0 + cT.localidx[f]) : (uint8_t)BC_UNIFORM;
+            }
+            S.bcode[((size_t)env * 4 + o) * PID_STRIDE + p] = code;
+        }
+    }
+    z = wave_xor(z);
+    static constexpr int8_t kCounts[12] = {1, 3, 2, 1, 1, 2, 2, 2, 2, 3, 3, 3};
+    if (l < 48) {
+        for (int o = 0; o < 4; ++o) {
+            const int s = l / 12, t = l % 12;
+            const bool tracked_seat = s != o && ((s & 1) != (o & 1));
+            S.rem[((size_t)env * 4 + o) * 48 + l] = tracked_seat ? kCounts[t] : 0;
+        }
+    }
+    if (l < 4) {
+        uint8_t trk = 0;
+        for (int s = 0; s < 4; ++s) if (s != l && ((s & 1) != (l & 1))) trk |= (uint8_t)(1u << s);
+        S.remtrk[(size_t)env * 4 + l] = trk;
+    }
+    if (l == 0) {
+        const uint64_t *Z = S.ztab;
+        const int w = S.winner[env];
+        z ^= Z[ZOFF_TURN + S.turn[env]] ^ Z[ZOFF_MC + (S.mc[env] & 0xFFF)] ^ Z[ZOFF_MSLC + (S.mslc[env] & 0x1FF)];
+        z ^= Z[ZOFF_WIN + (w < 0 ? 0 : w + 1)] ^ Z[ZOFF_SHOW + S.show_mode];
+        if (S.term[env]) z ^= Z[ZOFF_TERM];
+        if (S.draw[env]) z ^= Z[ZOFF_DRAW];
+        for (int s = 0; s < 4; ++s) {
+            if ((S.sdead[env] >> s) & 1) z ^= Z[ZOFF_SDEAD + s];
+            if ((S.sflag[env] >> s) & 1) z ^= Z[ZOFF_SFLAG + s];
+        }
+        S.zob[env] = z;
+    }
+}
+
+// ------------------------------------------------------------------ legal
+// Per env: masks of the acting seat's movable pieces (lanes = pieces), engineer
+// closures, counts, the packed canonical mask and the CSR scratch in ascending
+// source order (move_gen.py:1199 sorts the ids).
+__global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict__ acting,
+                                              int32_t *__restrict__ counts, int32_t *__restrict__ mask_words,
+                                              uint8_t *__restrict__ mask_bool)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    __shared__ int8_t cell[CELL_STRIDE];
+    __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
+    const int seat = acting ? acting[env] : S.turn[env];
+    const bool off = S.term[env] || seat < 0 || seat > 3 || ((S.sdead[env] >> (seat & 3)) & 1);
+    for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
+    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
+    __syncthreads();
+    const int team = seat & 1;
+    bool mov = false, eng = false;
+    int src = -1;
+    uint64_t m0 = 0, m1 = 0, m2 = 0;
+    if (!off && l < 30) {
+        const int pid = seat * 30 + l;
+        src = S.pos[(size_t)env * PID_STRIDE + pid];
+        const int t = S.ptype[(size_t)env * PID_STRIDE + pid];
+        mov = src >= 0 && t != T_JUNQI && t != T_DILEI && !is_sh(src);
+        if (mov) {
+            eng = t == T_GONGB;
+            piece_mask_lane(cell, src, team, eng, m0, m1, m2);
+        }
+    }
+    uint64_t engs = __ballot(mov && eng && is_rail(src < 0 ? 0 : src));
+    while (engs) {
+        const int e = __builtin_ctzll(engs);
+        engs &= engs - 1;
+        const int esrc = __shfl(src, e);
+        uint64_t e0, e1, e2;
+        engineer_mask(cell, esrc, team, e0, e1, e2);
+        if (l == e) { m0 |= e0; m1 |= e1; m2 |= e2; }
+    }
+    const int cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
+    // rank of this piece's source cell among the movable pieces
+    int rank = 0;
+    for (int j = 0; j < 30; ++j) {
+        const int oj = __shfl(src, j);
+        const bool mj = __shfl((int)mov, j) != 0;
+        rank += (mov && mj && oj < src) ? 1 : 0;
+    }
+    const int nmov = __popcll(__ballot(mov));
+    const int total = wave_sum(mov ? cnt : 0);
+    if (mov) {
+        S.lg_src[(size_t)env * 32 + rank] = (int16_t)src;
+        uint64_t *mk = S.lg_mask + ((size_t)env * 32 + rank) * 3;
+        mk[0] = m0; mk[1] = m1; mk[2] = m2;
+        // canonical compact mask bits (gpu_rollout.py:1220-1238 layout)
+        if (mask_words || mask_bool) {
+            const int cs = cT.rotc[seat][cT.f2c[src]] * NONB;
+            uint64_t w[3] = {m0, m1, m2};
+            for (int q = 0; q < 3; ++q) {
+                uint64_t x = w[q];
+                while (x) {
+                    const int b = __builtin_ctzll(x) + 64 * q;
+                    x &= x - 1;
+                    const int bit = cs + cT.rotc[seat][b];
+                    atomicOr(&bits[bit >> 5], 1u << (bit & 31));
+                }
+            }
+        }
+    }
+    if (l == 0) {
+        S.lg_n[env] = nmov;
+        S.lg_seat[env] = (int8_t)seat;
+        if (counts) counts[env] = total;
+    }
+    __syncthreads();
+    if (mask_words)
+        for (int w = l; w < JQ_MASK_WORDS; w += 64) mask_words[(size_t)env * JQ_MASK_WORDS + w] = (int32_t)bits[w];
+    if (mask_bool) {
+        uint8_t *row = mask_bool + (size_t)env * JQ_ACTION_DIM;
+        // bytes until the first 16-byte boundary, then whole 16-byte chunks, then the tail
+        const int mis = (int)((uintptr_t)row & 15);
+        const int head = mis ? 16 - mis : 0;
+        for (int i = l; i < head; i += 64) row[i] = (bits[i >> 5] >> (i & 31)) & 1;
+        const int nchunks = (JQ_ACTION_DIM - head) / 16;
+        for (int q = l; q < nchunks; q += 64) {
+            const int i0 = head + q * 16;
+            uint32_t v[4];
+            for (int k = 0; k < 4; ++k) {
+                uint32_t word = 0;
+                for (int b = 0; b < 4; ++b) {
+                    const int i = i0 + k * 4 + b;
+                    word |= ((bits[i >> 5] >> (i & 31)) & 1u) << (8 * b);
+                }
+                v[k] = word;
+            }
+            *reinterpret_cast<uint4 *>(row + i0) = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+        for (int i = head + nchunks * 16 + l; i < JQ_ACTION_DIM; i += 64) row[i] = (bits[i >> 5] >> (i & 31)) & 1;
+    }
+}
+
+// Exclusive scan of counts into offsets (N+1); one block.
+__global__ __launch_bounds__(1024) void k_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets, int n)
+{
+    __shared__ int32_t part[1024];
+    const int t = threadIdx.x;
+    const int per = (n + 1023) / 1024;
+    const int b = t * per, e = min(n, b + per);
+    int s = 0;
+    for (int i = b; i < e; ++i) s += counts[i];
+    part[t] = s;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int v = t >= o ? part[t - o] : 0;
+        __syncthreads();
+        part[t] += v;
+        __syncthreads();
+    }
+    int run = t ? part[t - 1] : 0;
+    for (int i = b; i < e; ++i) { offsets[i] = run; run += counts[i]; }
+    if (t == 1023) offsets[n] = part[1023];
+}
+
+// Write each env's ids at its offset: pieces in ascending source order, each
+// piece's destinations ascending (compact order = flat order).
+__global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict__ offsets, int32_t *__restrict__ values)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    const int n = S.lg_n[env];
+    int cnt = 0, src = 0;
+    uint64_t m[3] = {0, 0, 0};
+    if (l < n) {
+        src = S.lg_src[(size_t)env * 32 + l];
+        const uint64_t *mk = S.lg_mask + ((size_t)env * 32 + l) * 3;
+        m[0] = mk[0]; m[1] = mk[1]; m[2] = mk[2];
+        cnt = __popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]);
+    }
+    int incl = cnt;
+    for (int o = 1; o < 64; o <<= 1) { const int v = __shfl_up(incl, o); if (l >= o) incl += v; }
+    int w = offsets[env] + incl - cnt;
+    if (l < n) {
+        for (int q = 0; q < 3; ++q) {
+            uint64_t x = m[q];
+            while (x) {
+                const int b = __builtin_ctzll(x) + 64 * q;
+                x &= x - 1;
+                values[w++] = src * NC + cT.c2f[b];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ sampler
+__device__ __forceinline__ uint32_t philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                                 uint32_t k0, uint32_t k1)
+{   // Philox4x32-10 (Salmon et al., SC'11); returns the first output word
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0, hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+        c0 = hi1 ^ c1 ^ k0; c1 = lo1; c2 = hi0 ^ c3 ^ k1; c3 = lo0;
+        k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+    }
+    return c0;
+}
+
+__global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
+                         const int32_t *__restrict__ values, uint64_t seed, uint64_t ply, int32_t *__restrict__ out)
+{
+    const int env = blockIdx.x * blockDim.x + threadIdx.x;
+    if (env >= n) return;
+    const int c = counts[env];
+    if (c <= 0) { out[env] = -1; return; }
+    const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
+                                     (uint32_t)seed, (uint32_t)(seed >> 32));
+    const int idx = (int)(((uint64_t)u * (uint64_t)c) >> 32);
+    out[env] = values[offsets[env] + idx];
+}
+
+}  // namespace jq

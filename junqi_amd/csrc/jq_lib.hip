@@ -1,0 +1,501 @@
+// C ABI of the batched Junqi environment: handle lifetime, table upload, state
+// import/export and kernel launches. Declarations and contracts live in
+// include/junqi_amd.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/junqi_amd.h"
+#include "jq_device.h"
+#include "jq_kernels.h"
+#include "jq_obs.h"
+#include "jq_topology.h"
+
+using namespace jq;
+
+struct jq_env {
+    int device = 0;
+    State S{};
+    std::vector<void *> allocs;
+    bool zob_ready = false, rlut_ready = false;
+    int32_t *tmp_actions = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess) return fail(JQ_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+std::mutex g_tab_mu;
+bool g_tab_done[64] = {};
+Tables g_tables;
+bool g_host_tables = false;
+uint8_t g_bval[BC_COUNT][12];
+float g_decode[256];
+
+void prior_row(int slot, float out[12])
+{   // info_model.py:115-132: counts over the admissible types, float32 normalised
+    static const int cnt[14] = {0, 0, 1, 3, 2, 1, 1, 2, 2, 2, 2, 3, 3, 3};
+    const bool camp = slot == 6 || slot == 8 || slot == 12 || slot == 16 || slot == 18;
+    const bool sh = slot == 26 || slot == 28;
+    float v[12] = {};
+    if (!camp)
+        for (int t = 2; t <= 13; ++t) {
+            bool ok = true;
+            if (!sh) {
+                if (t == 2) ok = false;
+                if (t == 3 && slot < 20) ok = false;
+                if (t == 4 && slot < 5) ok = false;
+            }
+            if (ok) v[t - 2] = (float)cnt[t];
+        }
+    float s = 0.f;
+    for (float x : v) s += x;
+    for (int i = 0; i < 12; ++i) out[i] = s > 0.f ? v[i] / s : 0.f;
+}
+
+void build_host_tables()
+{
+    if (g_host_tables) return;
+    build_tables(g_tables);
+    std::memset(g_decode, 0, sizeof g_decode);
+    g_decode[0] = 0.f; g_decode[1] = 1.f; g_decode[2] = -1.f;
+    g_decode[3] = 1.0f / 3.0f; g_decode[4] = 2.0f / 3.0f;
+    int next = 5;
+    for (int code = 0; code < BC_COUNT; ++code) {
+        float row[12] = {};
+        if (code >= 1 && code <= 12) row[code - 1] = 1.f;
+        else if (code >= BC_PRIOR0 && code < BC_PRIOR0 + 30) prior_row(code - BC_PRIOR0, row);
+        else if (code == BC_UNIFORM) for (float &x : row) x = (float)(1.0 / 12.0);
+        for (int t = 0; t < 12; ++t) {
+            int found = -1;
+            for (int i = 0; i < next; ++i)
+                if (std::memcmp(&g_decode[i], &row[t], 4) == 0) { found = i; break; }
+            if (found < 0) { found = next; g_decode[next++] = row[t]; }
+            g_bval[code][t] = (uint8_t)found;
+        }
+    }
+    g_host_tables = true;
+}
+
+int ensure_device_tables(int device)
+{
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    build_host_tables();
+    if (device < 0 || device >= 64) return fail(JQ_E_ARG, "device %d out of range", device);
+    if (g_tab_done[device]) return JQ_OK;
+    HIP_TRY(hipMemcpyToSymbol(HIP_SYMBOL(cT), &g_tables, sizeof g_tables));
+    HIP_TRY(hipMemcpyToSymbol(HIP_SYMBOL(cBVAL), g_bval, sizeof g_bval));
+    HIP_TRY(hipMemcpyToSymbol(HIP_SYMBOL(cDECODE), g_decode, sizeof g_decode));
+    g_tab_done[device] = true;
+    return JQ_OK;
+}
+
+template <class T>
+int dalloc(jq_env *e, T *&p, size_t count, int fill_byte)
+{
+    void *q = nullptr;
+    const size_t bytes = count * sizeof(T) + 64;
+    if (hipMalloc(&q, bytes) != hipSuccess) return fail(JQ_E_OOM, "hipMalloc(%zu) failed", bytes);
+    e->allocs.push_back(q);
+    if (hipMemset(q, fill_byte, bytes) != hipSuccess) return fail(JQ_E_HIP, "hipMemset failed");
+    p = static_cast<T *>(q);
+    return JQ_OK;
+}
+
+struct FieldDesc { int elems, bytes; };
+const FieldDesc kFields[JQ_F_COUNT] = {
+    {CELL_STRIDE, 1}, {PID_STRIDE, 1}, {PID_STRIDE, 2}, {PID_STRIDE, 2}, {PID_STRIDE, 2}, {PID_STRIDE, 2},
+    {PID_STRIDE, 2}, {PID_STRIDE, 1}, {PID_STRIDE, 2}, {PID_STRIDE, 2}, {4 * PID_STRIDE, 1}, {4 * 48, 1},
+    {4, 1},
+    {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 2},
+    {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 8},
+    {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 1}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 1},
+    {HIST_LEN, 4}, {1, 4}, {1, 1}, {1, 1}, {1, 1}, {1, 1}, {1, 1}, {1, 1}, {1, 4}, {1, 4}, {1, 8},
+};
+
+void *field_base(jq_env *e, int f)
+{
+    State &S = e->S;
+    switch (f) {
+    case JQ_F_CELL: return S.cell;
+    case JQ_F_PTYPE: return S.ptype;
+    case JQ_F_POS: return S.pos;
+    case JQ_F_ZERO: return S.zero;
+    case JQ_F_MOVE_COUNT: return S.mcount;
+    case JQ_F_ACTIVE_EAT: return S.aeat;
+    case JQ_F_PASSIVE_SURV: return S.psurv;
+    case JQ_F_DEATH_REASON: return S.dreason;
+    case JQ_F_DEATH_STEP: return S.dstep;
+    case JQ_F_DEATH_LOC: return S.dloc;
+    case JQ_F_BELIEF: return S.bcode;
+    case JQ_F_REMAINING: return S.rem;
+    case JQ_F_REM_TRACKED: return S.remtrk;
+    case JQ_F_CM_DIRECT_LO: return S.cm_dlo;
+    case JQ_F_CM_DIRECT_HI: return S.cm_dhi;
+    case JQ_F_CM_DIRECT_TYPE: return S.cm_dtype;
+    case JQ_F_CM_LAST_DIRECT: return S.cm_ldir;
+    case JQ_F_CM_OTHER_COUNT: return S.cm_ocnt;
+    case JQ_F_CM_CHAIN_LO: return S.cm_clo;
+    case JQ_F_CM_CHAIN_HI: return S.cm_chi;
+    case JQ_F_CM_CHAIN_TYPE: return S.cm_ctype;
+    case JQ_F_CM_LAST_CHAIN: return S.cm_lchain;
+    case JQ_F_CM_EATEN_LO: return S.cm_elo;
+    case JQ_F_CM_EATEN_HI: return S.cm_ehi;
+    case JQ_F_CM_FLOOR: return S.cm_floor;
+    case JQ_F_CM_FLOOR_STEP: return S.cm_fstep;
+    case JQ_F_CM_FLAGS: return S.cm_flags;
+    case JQ_F_HIST: return S.hist;
+    case JQ_F_HIST_META: return S.hmeta;
+    case JQ_F_TURN: return S.turn;
+    case JQ_F_TERMINATED: return S.term;
+    case JQ_F_WINNER: return S.winner;
+    case JQ_F_DRAW: return S.draw;
+    case JQ_F_SEAT_DEAD: return S.sdead;
+    case JQ_F_FLAG_REV: return S.sflag;
+    case JQ_F_MOVE_COUNTER: return S.mc;
+    case JQ_F_MSLC: return S.mslc;
+    case JQ_F_ZOBRIST: return S.zob;
+    default: return nullptr;
+    }
+}
+
+inline hipStream_t strm(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+int check_env(jq_env *e)
+{
+    if (!e) return fail(JQ_E_ARG, "null handle");
+    if (hipSetDevice(e->device) != hipSuccess) return fail(JQ_E_HIP, "hipSetDevice(%d) failed", e->device);
+    return JQ_OK;
+}
+
+int launch_check(const char *what)
+{
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(JQ_E_HIP, "%s launch: %s", what, hipGetErrorString(err));
+    return JQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *jq_last_error(void) { return g_err.c_str(); }
+const char *jq_version(void) { return "junqi_amd 0.1 (gfx950)"; }
+
+int jq_create(jq_env **out, int32_t n, int32_t max_num_moves, int32_t show_mode, int32_t device)
+{
+    if (!out) return fail(JQ_E_ARG, "out is null");
+    *out = nullptr;
+    if (n <= 0 || n > (1 << 24)) return fail(JQ_E_ARG, "num_envs %d out of range", n);
+    if (max_num_moves <= 0) return fail(JQ_E_ARG, "max_num_moves must be positive");
+    if (show_mode < 0 || show_mode > 2) return fail(JQ_E_ARG, "show_mode %d not in {0,1,2}", show_mode);
+    int ndev = 0;
+    HIP_TRY(hipGetDeviceCount(&ndev));
+    if (device < 0 || device >= ndev) return fail(JQ_E_ARG, "device %d not present (%d devices)", device, ndev);
+    HIP_TRY(hipSetDevice(device));
+    int rc = ensure_device_tables(device);
+    if (rc) return rc;
+    jq_env *e = new jq_env();
+    e->device = device;
+    State &S = e->S;
+    S.n = n; S.max_moves = max_num_moves; S.show_mode = show_mode; S.pool_size = 0;
+    const size_t N = (size_t)n;
+#define A(ptr, cnt, fill) do { if ((rc = dalloc(e, ptr, cnt, fill)) != 0) { jq_destroy(e); return rc; } } while (0)
+    A(S.cell, N * CELL_STRIDE, 0xFF);
+    A(S.ptype, N * PID_STRIDE, 0xFF);
+    A(S.pos, N * PID_STRIDE, 0xFF);
+    A(S.zero, N * PID_STRIDE, 0xFF);
+    A(S.mcount, N * PID_STRIDE, 0); A(S.aeat, N * PID_STRIDE, 0); A(S.psurv, N * PID_STRIDE, 0);
+    A(S.dreason, N * PID_STRIDE, 0xFF); A(S.dstep, N * PID_STRIDE, 0xFF); A(S.dloc, N * PID_STRIDE, 0xFF);
+    A(S.bcode, N * 4 * PID_STRIDE, 0);
+    A(S.rem, N * 4 * 48, 0);
+    A(S.remtrk, N * 4, 0);
+    const size_t C = N * 4 * PID_STRIDE;
+    A(S.cm_dlo, C, 0); A(S.cm_dhi, C, 0); A(S.cm_clo, C, 0); A(S.cm_chi, C, 0); A(S.cm_elo, C, 0); A(S.cm_ehi, C, 0);
+    A(S.cm_dtype, C, 0); A(S.cm_ctype, C, 0);
+    A(S.cm_ldir, C, 0xFF); A(S.cm_ocnt, C, 0); A(S.cm_lchain, C, 0xFF); A(S.cm_fstep, C, 0xFF);
+    A(S.cm_floor, C, 0); A(S.cm_flags, C, 0);
+    A(S.hist, N * HIST_LEN, 0); A(S.hmeta, N, 0);
+    A(S.turn, N, 0); A(S.term, N, 0); A(S.winner, N, 0xFF); A(S.draw, N, 0);
+    A(S.sdead, N, 0); A(S.sflag, N, 0); A(S.mc, N, 0); A(S.mslc, N, 0); A(S.zob, N, 0);
+    A(S.lg_src, N * 32, 0); A(S.lg_mask, N * 32 * 3, 0); A(S.lg_n, N, 0); A(S.lg_seat, N, 0);
+    A(e->tmp_actions, N, 0);
+    uint64_t *zt = nullptr; A(zt, (size_t)ZTOTAL, 0); S.ztab = zt;
+    float *rl = nullptr; A(rl, 4 * 4096, 0); S.rlut = rl;
+#undef A
+    *out = e;
+    return JQ_OK;
+}
+
+int jq_destroy(jq_env *e)
+{
+    if (!e) return JQ_OK;
+    (void)hipSetDevice(e->device);
+    for (void *p : e->allocs) (void)hipFree(p);
+    delete e;
+    return JQ_OK;
+}
+
+int32_t jq_num_envs(const jq_env *e) { return e ? e->S.n : 0; }
+
+int jq_upload_zobrist(jq_env *e, const uint64_t *host, int64_t count)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!host || count != ZTOTAL) return fail(JQ_E_ARG, "zobrist table must hold %d uint64 values", ZTOTAL);
+    HIP_TRY(hipMemcpy((void *)e->S.ztab, host, sizeof(uint64_t) * ZTOTAL, hipMemcpyHostToDevice));
+    e->zob_ready = true;
+    return JQ_OK;
+}
+
+int jq_upload_recency(jq_env *e, const float *host)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!host) return fail(JQ_E_ARG, "null recency table");
+    HIP_TRY(hipMemcpy((void *)e->S.rlut, host, sizeof(float) * 4 * 4096, hipMemcpyHostToDevice));
+    e->rlut_ready = true;
+    return JQ_OK;
+}
+
+int jq_upload_setup_pool(jq_env *e, const int8_t *host, int32_t pool_size)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!host || pool_size <= 0) return fail(JQ_E_ARG, "empty setup pool");
+    int8_t *p = nullptr;
+    if ((rc = dalloc(e, p, (size_t)pool_size * NP, 0)) != 0) return rc;
+    HIP_TRY(hipMemcpy(p, host, (size_t)pool_size * NP, hipMemcpyHostToDevice));
+    e->S.pool = p;
+    e->S.pool_size = pool_size;
+    return JQ_OK;
+}
+
+int jq_reset_lineups(jq_env *e, const int8_t *host, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!host) return fail(JQ_E_ARG, "null lineups");
+    if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before resetting");
+    int8_t *d = nullptr;
+    const size_t bytes = (size_t)e->S.n * NP;
+    HIP_TRY(hipMallocAsync((void **)&d, bytes, strm(stream)));
+    HIP_TRY(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, strm(stream)));
+    hipLaunchKernelGGL(k_reset_lineups, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, d);
+    rc = launch_check("k_reset_lineups");
+    HIP_TRY(hipFreeAsync(d, strm(stream)));
+    HIP_TRY(hipStreamSynchronize(strm(stream)));
+    return rc;
+}
+
+int jq_generate_pool(int64_t seed, int32_t pool_size, int8_t *host_out)
+{
+    if (!host_out || pool_size < 0) return fail(JQ_E_ARG, "bad pool buffer");
+    generate_pool((uint64_t)seed, pool_size, host_out);
+    return JQ_OK;
+}
+
+int jq_board_tables(void *host_out, int64_t nbytes)
+{
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    build_host_tables();
+    if (!host_out || nbytes != (int64_t)sizeof(Tables)) return fail(JQ_E_ARG, "need %zu bytes", sizeof(Tables));
+    std::memcpy(host_out, &g_tables, sizeof(Tables));
+    return JQ_OK;
+}
+
+int jq_generate_lineups(int64_t seed_base, int32_t count, int8_t *host_out)
+{
+    if (!host_out || count < 0) return fail(JQ_E_ARG, "bad lineup buffer");
+    for (int32_t i = 0; i < count; ++i) generate_setup((uint64_t)(seed_base + i), host_out + (size_t)i * NP);
+    return JQ_OK;
+}
+
+int jq_reset_seeded(jq_env *e, int64_t seed_base, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    std::vector<int8_t> lu((size_t)e->S.n * NP);
+    if ((rc = jq_generate_lineups(seed_base, e->S.n, lu.data())) != 0) return rc;
+    return jq_reset_lineups(e, lu.data(), stream);
+}
+
+int jq_reset_terminated(jq_env *e, int64_t seed, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!e->S.pool || e->S.pool_size <= 0) return fail(JQ_E_STATE, "no setup pool uploaded");
+    if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before resetting");
+    hipLaunchKernelGGL(k_reset_terminated, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, seed);
+    return launch_check("k_reset_terminated");
+}
+
+int jq_step(jq_env *e, const int32_t *actions, const int8_t *acting, int32_t fmt, uint8_t *valid, int8_t *event,
+            uint8_t *terminated, int8_t *winner, uint8_t *draw, uint8_t *flag_captured, uint8_t *seats_died,
+            float *reward, int32_t *world_action, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!actions) return fail(JQ_E_ARG, "null actions");
+    if (fmt != JQ_ACT_WORLD && fmt != JQ_ACT_CANONICAL) return fail(JQ_E_ARG, "bad action format %d", fmt);
+    if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before stepping");
+    StepOut O{valid, event, terminated, winner, draw, flag_captured, seats_died, reward, world_action};
+    hipLaunchKernelGGL(k_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, actions, acting, fmt, O);
+    return launch_check("k_step");
+}
+
+int jq_legal(jq_env *e, const int8_t *acting, int32_t *counts, int32_t *offsets, int32_t *values,
+             int32_t *mask_words, uint8_t *mask_bool, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if ((offsets || values) && !counts) return fail(JQ_E_ARG, "offsets/values need counts");
+    if (values && !offsets) return fail(JQ_E_ARG, "values need offsets");
+    hipLaunchKernelGGL(k_legal, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, acting, counts, mask_words, mask_bool);
+    if ((rc = launch_check("k_legal")) != 0) return rc;
+    if (offsets) {
+        hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, strm(stream), counts, offsets, e->S.n);
+        if ((rc = launch_check("k_scan")) != 0) return rc;
+    }
+    if (values) {
+        hipLaunchKernelGGL(k_emit, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, offsets, values);
+        if ((rc = launch_check("k_emit")) != 0) return rc;
+    }
+    return JQ_OK;
+}
+
+int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial, float *aux,
+               float *global, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!spatial) return fail(JQ_E_ARG, "null spatial output");
+    if (fmt == JQ_OBS_U8 && !e->rlut_ready && aux) return fail(JQ_E_STATE, "recency table not uploaded");
+    if (fmt != JQ_OBS_U8 && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
+    const dim3 grid(all_seats ? e->S.n * 4 : e->S.n), block(OBS_THREADS);
+    switch (fmt) {
+    case JQ_OBS_F32: hipLaunchKernelGGL(k_observe<0>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global); break;
+    case JQ_OBS_BF16: hipLaunchKernelGGL(k_observe<1>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global); break;
+    case JQ_OBS_U8: hipLaunchKernelGGL(k_observe<2>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global); break;
+    default: return fail(JQ_E_ARG, "bad observation format %d", fmt);
+    }
+    return launch_check("k_observe");
+}
+
+int jq_obs_decode_table(float *out)
+{
+    if (!out) return fail(JQ_E_ARG, "null output");
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    build_host_tables();
+    std::memcpy(out, g_decode, sizeof g_decode);
+    return JQ_OK;
+}
+
+int jq_sample_uniform(jq_env *e, const int32_t *counts, const int32_t *offsets, const int32_t *values, uint64_t seed,
+                      uint64_t ply, int32_t *out, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!counts || !offsets || !values || !out) return fail(JQ_E_ARG, "null sampler buffer");
+    hipLaunchKernelGGL(k_sample, dim3((e->S.n + 255) / 256), dim3(256), 0, strm(stream), e->S.n, counts, offsets,
+                       values, seed, ply, out);
+    return launch_check("k_sample");
+}
+
+int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_t ply, int64_t reset_seed,
+                int32_t *counts, int32_t *offsets, int32_t *values, int32_t *mask_words, int32_t obs_fmt,
+                void *spatial, float *aux, float *global, uint8_t *terminated, float *reward, int32_t *actions_out,
+                void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    const int32_t *act = actions;
+    if (!act) {
+        int32_t *dst = actions_out ? actions_out : e->tmp_actions;
+        if ((rc = jq_sample_uniform(e, counts, offsets, values, sample_seed, ply, dst, stream)) != 0) return rc;
+        act = dst;
+    }
+    if ((rc = jq_step(e, act, nullptr, JQ_ACT_WORLD, nullptr, nullptr, terminated, nullptr, nullptr, nullptr,
+                      nullptr, reward, nullptr, stream)) != 0)
+        return rc;
+    if (e->S.pool && (rc = jq_reset_terminated(e, reset_seed, stream)) != 0) return rc;
+    if ((rc = jq_legal(e, nullptr, counts, offsets, values, mask_words, nullptr, stream)) != 0) return rc;
+    if (spatial && (rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream)) != 0) return rc;
+    return JQ_OK;
+}
+
+int jq_field_info(int32_t f, int32_t *elems, int32_t *bytes)
+{
+    if (f < 0 || f >= JQ_F_COUNT) return fail(JQ_E_ARG, "bad field %d", f);
+    if (elems) *elems = kFields[f].elems;
+    if (bytes) *bytes = kFields[f].bytes;
+    return JQ_OK;
+}
+
+int jq_get_field(jq_env *e, int32_t f, void *host)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (f < 0 || f >= JQ_F_COUNT || !host) return fail(JQ_E_ARG, "bad field %d", f);
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(host, field_base(e, f), (size_t)e->S.n * kFields[f].elems * kFields[f].bytes, hipMemcpyDeviceToHost));
+    return JQ_OK;
+}
+
+int jq_set_field(jq_env *e, int32_t f, const void *host)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (f < 0 || f >= JQ_F_COUNT || !host) return fail(JQ_E_ARG, "bad field %d", f);
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(field_base(e, f), host, (size_t)e->S.n * kFields[f].elems * kFields[f].bytes, hipMemcpyHostToDevice));
+    return JQ_OK;
+}
+
+int jq_field_ptr(jq_env *e, int32_t f, void **ptr)
+{
+    if (!e || !ptr || f < 0 || f >= JQ_F_COUNT) return fail(JQ_E_ARG, "bad field %d", f);
+    *ptr = field_base(e, f);
+    return JQ_OK;
+}
+
+int jq_finalize_import(jq_env *e, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables first");
+    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S);
+    if ((rc = launch_check("k_finalize")) != 0) return rc;
+    HIP_TRY(hipStreamSynchronize(strm(stream)));
+    return JQ_OK;
+}
+
+int jq_sync(void *stream)
+{
+    HIP_TRY(hipStreamSynchronize(strm(stream)));
+    return JQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Host-built constant tables of the 17x17 Junqi board, uploaded once per device.
+//
+// Derived from the board's closed forms: seat rectangles, camps, strongholds,
+// the rail ring of each seat, the nine-grid with its two-step links and the four
+// corner arcs (reference junqi_core/board.py:88-279, rail_topology.py:60-276,
+// _movegen_tables.py:155-467). Layouts are chosen for the device: rail cells are
+// re-indexed 0..72 so an engineer's reachable set fits two 64-bit ballots.
+#pragma once
+#include <cstdint>
+
+namespace jq {
+
+constexpr int NC = 289;
+constexpr int NONB = 129;
+constexpr int NRAIL = 73;
+constexpr int NP = 120;
+
+// cell flag bits
+enum : uint16_t {
+    CF_ON = 1u << 0, CF_RAIL = 1u << 1, CF_CAMP = 1u << 2, CF_SH = 1u << 3,
+    CF_NG = 1u << 4, CF_ARC = 1u << 5,
+};
+
+struct Tables {
+    uint16_t cflags[NC];          // CF_* | curve_id << 8
+    int16_t adj[NC][4];           // +x,-x,+y,-y on-board neighbours, -1 none
+    int16_t diag[NC][4];          // diagonal neighbours with a camp endpoint, -1 none
+    int8_t railidx[NC];           // rail index 0..72 or -1
+    int16_t railcell[NRAIL];      // rail index -> flat
+    uint64_t rnbr[NRAIL][2];      // rail-graph neighbour set as a 73-bit mask
+    int16_t rays[NRAIL][4][12];   // straight rail runs per direction (-1 pad)
+    int8_t raylen[NRAIL][4];
+    int16_t crays[NRAIL][2][11];  // curve-rail chain runs both ways (-1 pad)
+    int8_t craylen[NRAIL][2];
+    int16_t f2c[NC];              // flat -> compact (-1 off board)
+    int16_t c2f[NONB];
+    int16_t rot[4][NC];           // world flat -> canonical flat of observer s
+    int16_t unrot[4][NC];         // canonical flat -> world flat
+    uint8_t rotc[4][NONB];        // world compact -> canonical compact
+    int16_t home[NP];             // pid -> initial flat (-1 for camp slots)
+    int8_t slotch[30];            // seat slot -> piece_slot plane (-1 camps)
+    uint8_t statics[NC];          // board_static planes 0..4 as bits
+    int16_t sh_other[NC];         // stronghold cell -> the other stronghold of that seat
+    int8_t owner[NC];             // owning seat or -1
+    int8_t localidx[NC];          // slot index in the owner's rectangle or -1
+};
+
+void build_tables(Tables &t);
+void seat_cell(int seat, int slot, int &x, int &y);
+
+// CPython random.Random(seed) lineup stream of junqi_core.setup.generate_random_setup
+// (setup.py:162-258): four lineups of 30 piece types per seed.
+void generate_setup(uint64_t seed, int8_t out[120]);
+// pool_size setups from one random.Random(seed) stream (junqi_rl/gpu_rollout.py:255-275)
+void generate_pool(uint64_t seed, int pool_size, int8_t *out);
+
+}  // namespace jq

@@ -13,7 +13,8 @@ obs_hashes.json                    reference tests/golden/obs_hashes.json (12 re
 replay_recovered.json              compact per-ply record of
                                    replays/recovered_20260815 (lineups, actions,
                                    per-ply result and state_after fields)
-recency_lut_f32.bin                float32 exp(-e/tau) for e in [0,4096),
+recency_lut_f32.bin                float32 exp(-e/tau) for e in [0,4096) (also written to
+                                   junqi_amd/data/, where the library loads it),
                                    tau planes (32, 256, 64, 128), computed the way
                                    junqi_core/observation.py:1561-1562 does
 zobrist_sha256.txt                 SHA-256 of the numpy PCG64 Zobrist stream
@@ -101,6 +102,7 @@ def main() -> None:
     shutil.copyfile(ref / "tests" / "golden" / "obs_hashes.json", HERE / "obs_hashes.json")
     (HERE / "replay_recovered.json").write_text(json.dumps(replay(ref)))
     recency_lut().tofile(HERE / "recency_lut_f32.bin")
+    recency_lut().tofile(HERE.parent.parent / "junqi_amd" / "data" / "recency_lut_f32.bin")
     z = zobrist_stream()
     (HERE / "zobrist_sha256.txt").write_text(
         f"{hashlib.sha256(z.astype('<u8').tobytes()).hexdigest()}  {z.size} uint64 (little-endian)\n")

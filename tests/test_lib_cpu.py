@@ -1,0 +1,128 @@
+"""CPU-side checks of the HIP library: it loads, exports every declared symbol,
+and its host-built tables and lineup streams equal the oracle's."""
+
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+@pytest.fixture(scope="module")
+def jl():
+    from junqi_amd import _lib
+    return _lib
+
+
+def test_every_declared_symbol_is_exported(jl):
+    header = (ROOT / "include" / "junqi_amd.h").read_text()
+    declared = set(re.findall(r"^(?:int|const char \*|int32_t)\s*\*?\s*(jq_\w+)\(", header, re.M))
+    assert declared, "no declarations found"
+    assert declared == set(jl.exported_symbols())
+    lib = C.CDLL(str(jl.LIB_PATH))
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_errors(jl):
+    assert b"gfx950" in jl.lib.jq_version()
+    assert jl.lib.jq_field_info(99, None, None) != 0
+    assert b"bad field" in jl.lib.jq_last_error()
+
+
+_TABLES = np.dtype([
+    ("cflags", "<u2", (289,)), ("adj", "<i2", (289, 4)), ("diag", "<i2", (289, 4)), ("railidx", "i1", (289,)),
+    ("railcell", "<i2", (73,)), ("rnbr", "<u8", (73, 2)), ("rays", "<i2", (73, 4, 12)), ("raylen", "i1", (73, 4)),
+    ("crays", "<i2", (73, 2, 11)), ("craylen", "i1", (73, 2)), ("f2c", "<i2", (289,)), ("c2f", "<i2", (129,)),
+    ("rot", "<i2", (4, 289)), ("unrot", "<i2", (4, 289)), ("rotc", "u1", (4, 129)), ("home", "<i2", (120,)),
+    ("slotch", "i1", (30,)), ("statics", "u1", (289,)), ("sh_other", "<i2", (289,)), ("owner", "i1", (289,)),
+    ("localidx", "i1", (289,)),
+], align=True)
+
+
+def _product_tables(jl):
+    buf = np.zeros(1, _TABLES)
+    assert jl.lib.jq_board_tables(buf.ctypes.data, _TABLES.itemsize) == 0, jl.lib.jq_last_error()
+    return buf[0]
+
+
+def test_board_tables_equal_oracle(jl):
+    t = _product_tables(jl)
+    o = O.tables()
+    fl = t["cflags"]
+    assert np.array_equal((fl & 1) > 0, o["on_board"] > 0)
+    assert np.array_equal((fl & 2) > 0, o["rail"] > 0)
+    assert np.array_equal((fl & 4) > 0, o["camp"] > 0)
+    assert np.array_equal((fl & 8) > 0, o["stronghold"] > 0)
+    assert np.array_equal((fl & 16) > 0, o["ninegrid"] > 0)
+    assert np.array_equal((fl & 32) > 0, o["arc"] > 0)
+    assert np.array_equal(fl >> 8, o["curve"])
+    assert np.array_equal(t["c2f"], o["compact_to_flat"])
+    # rail graph: the 73-bit neighbour masks against the oracle adjacency lists
+    for i in range(73):
+        f = int(t["railcell"][i])
+        got = {int(t["railcell"][j]) for j in range(73) if (int(t["rnbr"][i][j >> 6]) >> (j & 63)) & 1}
+        want = {int(v) for v in o["rail_adj"][f] if v >= 0}
+        assert got == want, f
+    # straight and curve runs reproduce the oracle's destinations on an empty board
+    g = O.Game.from_pieces([(0, 12, 8, 11)])
+    for i in range(73):
+        f = int(t["railcell"][i])
+        runs = set()
+        for k in range(4):
+            runs |= {int(c) for c in t["rays"][i][k][: t["raylen"][i][k]]}
+        for d in range(2):
+            runs |= {int(c) for c in t["crays"][i][d][: t["craylen"][i][d]]}
+        gg = O.Game.from_pieces([(0, 12, f % 17, f // 17)])
+        ids = {int(a) % 289 for a in gg.legal_ids(0)} if not (fl[f] & 8) else set()
+        road = {int(c) for c in t["adj"][f] if c >= 0} | {int(c) for c in t["diag"][f] if c >= 0}
+        if not (fl[f] & 8):
+            assert ids == runs | road, f
+    # rotations are bijections and match rotation.py's point map
+    for s in range(4):
+        assert sorted(t["rot"][s].tolist()) == list(range(289))
+        assert np.array_equal(t["unrot"][s][t["rot"][s]], np.arange(289))
+    assert t["rot"][1][8 * 17 + 3] == 13 * 17 + 8    # WEST's centre camp (3,8) -> (8,13)
+    assert t["rot"][3][8 * 17 + 13] == 13 * 17 + 8   # EAST's centre camp
+
+
+@pytest.mark.parametrize("seed", [0, 1, 42, 2026, 123456789])
+def test_lineups_equal_oracle(jl, seed):
+    from junqi_amd.batch import generate_lineups
+    got = generate_lineups(seed, 6)
+    for i in range(6):
+        assert np.array_equal(got[i], O.random_setup(seed + i))
+
+
+def test_pool_equals_oracle(jl):
+    from junqi_amd.batch import generate_pool
+    assert np.array_equal(generate_pool(42, 50), O.setup_pool(42, 50))
+
+
+def test_decode_table(jl):
+    from junqi_amd.batch import decode_table
+    d = decode_table()
+    assert d[0] == 0 and d[1] == 1 and d[2] == -1
+    assert d[3] == np.float32(1) / np.float32(3) and d[4] == np.float32(2) / np.float32(3)
+    vals = set(d[:32].tolist())
+    for code in list(range(1, 13)) + [16 + s for s in range(30)] + [64]:
+        for v in O.belief_row(code):
+            assert float(v) in vals
+
+
+def test_packaged_recency_table_is_the_fixture():
+    a = (ROOT / "junqi_amd" / "data" / "recency_lut_f32.bin").read_bytes()
+    b = (ROOT / "tests" / "golden" / "recency_lut_f32.bin").read_bytes()
+    assert a == b
+
+
+def test_zobrist_stream_matches_oracle(jl):
+    from junqi_amd.batch import zobrist_stream
+    assert np.array_equal(zobrist_stream(), O.zobrist_tables())
