@@ -48,7 +48,9 @@ def _play(jq, n, plies, show_mode, seed, check_every=1, obs_every=1, all_seats_e
     for ply in range(plies):
         if ply % 40 == 0:
             print(f"[play] ply {ply}", flush=True)
-        offs, vals = b.legal_csr_numpy()
+        b.legal()   # CSR and packed canonical mask in one call
+        offs = b.offsets.cpu().numpy()
+        vals = b.values[: int(offs[-1])].cpu().numpy()
         mw = b.mask_words.cpu().numpy()
         actions = np.zeros(n, np.int32)
         for i, g in enumerate(games):
