@@ -52,7 +52,11 @@ def _load() -> C.CDLL:
         raise ImportError(
             f"junqi_amd HIP library not built: {LIB_PATH} is missing "
             "(run `python junqi_amd/build.py` or __graft_entry__.build())")
-    L = C.CDLL(str(LIB_PATH))
+    return bind(C.CDLL(str(LIB_PATH)))
+
+
+def bind(L: C.CDLL) -> C.CDLL:
+    """Declare the C-ABI signatures of include/junqi_amd.h on a loaded library."""
     P, I32, I64, U64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64
     sig = {
         "jq_last_error": ([], C.c_char_p), "jq_version": ([], C.c_char_p),

@@ -14,7 +14,7 @@
 
 #include <cstdint>
 
-#include "../../include/junqi_amd.h"
+#include "junqi_amd.h"
 #include "jq_device.h"
 #include "jq_topology.h"
 

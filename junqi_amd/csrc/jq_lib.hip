@@ -3,6 +3,7 @@
 // include/junqi_amd.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -10,7 +11,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/junqi_amd.h"
+#include "junqi_amd.h"
 #include "jq_device.h"
 #include "jq_kernels.h"
 #include "jq_obs.h"
@@ -24,6 +25,7 @@ struct jq_env {
     std::vector<void *> allocs;
     bool zob_ready = false, rlut_ready = false;
     int32_t *tmp_actions = nullptr;
+    int obs_blocks[3] = {0, 0, 0};   // resident k_observe blocks on the device, per format
 };
 
 namespace {
@@ -195,6 +197,23 @@ int launch_check(const char *what)
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return fail(JQ_E_HIP, "%s launch: %s", what, hipGetErrorString(err));
     return JQ_OK;
+}
+
+// Persistent grid of k_observe<FMT>: every block the device can hold at once.
+template <int FMT>
+int obs_grid_fmt(jq_env *e)
+{
+    int per_cu = 0, cus = 0;
+    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_observe<FMT>, OBS_THREADS, 0));
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
+    e->obs_blocks[FMT] = std::max(1, per_cu) * std::max(1, cus);
+    return JQ_OK;
+}
+
+int obs_grid(jq_env *e, int fmt)
+{
+    if (e->obs_blocks[fmt] > 0) return JQ_OK;
+    return fmt == 0 ? obs_grid_fmt<0>(e) : fmt == 1 ? obs_grid_fmt<1>(e) : obs_grid_fmt<2>(e);
 }
 
 }  // namespace
@@ -392,14 +411,20 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
     int rc = check_env(e);
     if (rc) return rc;
     if (!spatial) return fail(JQ_E_ARG, "null spatial output");
-    if (fmt == JQ_OBS_U8 && !e->rlut_ready && aux) return fail(JQ_E_STATE, "recency table not uploaded");
-    if (fmt != JQ_OBS_U8 && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
-    const dim3 grid(all_seats ? e->S.n * 4 : e->S.n), block(OBS_THREADS);
+    if (fmt < JQ_OBS_F32 || fmt > JQ_OBS_U8) return fail(JQ_E_ARG, "bad observation format %d", fmt);
+    const int es = fmt == JQ_OBS_F32 ? 4 : fmt == JQ_OBS_BF16 ? 2 : 1;
+    if ((uintptr_t)spatial % es || (aux && (uintptr_t)aux % 4) || (global && (uintptr_t)global % 4))
+        return fail(JQ_E_ARG, "observation buffers must be aligned to their element size");
+    if ((fmt != JQ_OBS_U8 || aux) && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
+    const int nrows = all_seats ? e->S.n * 4 : e->S.n;
+    if ((rc = obs_grid(e, fmt)) != 0) return rc;
+    // u8 rows stream fast enough that the next row's gathers need hiding: persistent
+    // blocks prefetch them. The wider formats run one row per block.
+    const dim3 grid(fmt == JQ_OBS_U8 ? std::min(nrows, e->obs_blocks[fmt]) : nrows), block(OBS_THREADS);
     switch (fmt) {
-    case JQ_OBS_F32: hipLaunchKernelGGL(k_observe<0>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global); break;
-    case JQ_OBS_BF16: hipLaunchKernelGGL(k_observe<1>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global); break;
-    case JQ_OBS_U8: hipLaunchKernelGGL(k_observe<2>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global); break;
-    default: return fail(JQ_E_ARG, "bad observation format %d", fmt);
+    case JQ_OBS_F32: hipLaunchKernelGGL(k_observe<0>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
+    case JQ_OBS_BF16: hipLaunchKernelGGL(k_observe<1>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
+    default: hipLaunchKernelGGL(k_observe<2>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
     }
     return launch_check("k_observe");
 }

@@ -1,24 +1,29 @@
 // Observation encoder (included into jq_lib.hip's translation unit, which owns
-// the constant tables). One 256-thread block per (env, observer) row.
+// the constant tables).
 //
 // Layout and values follow junqi_core/observation.py:155-232 (317 planes in the
 // observer's canonical frame, 28 globals) and its writers at :908-1651.
 //
 // Every element of a row has a u8 value code (cDECODE maps codes to floats).
-// Only ~1-2k of the 91,613 elements are nonzero, so the block builds the row
-// sparsely in LDS and then streams it densely:
-//   * `bits`: one bit per element, bit 0 of its code (all 0/1 planes, move
-//     history destinations, ...), set by LDS atomic-OR scatter from the threads
-//     that own a piece, a history entry or a constant plane;
+// Only ~1-2k of the 91,613 elements are nonzero, so a row is built sparsely in
+// LDS and then streamed densely:
+//   * `bits`: one bit per element, bit 0 of its code (all 0/1 planes), set by
+//     LDS atomic-OR scatter from the threads that own a piece or a constant
+//     plane; the row-independent board_static words are copied from a template;
 //   * `img`: a byte image of the four plane ranges whose codes exceed 1
 //     (teammate / enemy beliefs, move history, kill_mine_count), placed so that
-//     the 16-byte output chunk at a given address reads an aligned 16-byte LDS
-//     word; zero outside the ranges.
+//     the 16-byte output chunk at a given address reads an aligned LDS word;
+//     zero outside the ranges and in 16-byte margins around them.
 // The emit loop gives each lane one aligned 16-byte chunk of the row per
 // iteration (a wave covers 1 KB of HBM), expands the chunk's bits to bytes
-// (u8), to bf16 or to f32, ORs in the image, and issues one 16-byte store.
+// (u8), bf16 or f32, merges the image and issues one 16-byte store. Whether a
+// wave's 1 KB span touches an image range is decided once per wave.
 // The six continuous planes (turn history, recency) are exact floats: they go
 // to the aux output in the u8 format and are computed per element in f32 / bf16.
+//
+// Blocks are persistent (grid = resident blocks): while a block streams row i
+// out, its threads already hold the loads of row i + gridDim.x in registers,
+// so the gather latency of the next build hides behind the current stores.
 #pragma once
 
 namespace jq {
@@ -40,7 +45,12 @@ constexpr int RG1_B = RG0_B + rg_bytes(RG0_S, RG0_E);
 constexpr int RG2_B = RG1_B + rg_bytes(RG1_S, RG1_E);
 constexpr int RG3_B = RG2_B + rg_bytes(RG2_S, RG2_E);
 constexpr int IMG_BYTES = RG3_B + rg_bytes(RG3_S, RG3_E);
+constexpr int IMG_ZERO = RG0_B;   // 16 bytes that are always zero (range 0's leading margin)
 static_assert(IMG_BYTES % 16 == 0, "image must be a whole number of 16-byte words");
+
+// board_static planes 58-63 occupy words 523..577 of `bits`; the template keeps
+// 16-byte-aligned words 520..579
+constexpr int STAT_Q0 = 130, STAT_NQ = 15;
 
 // continuous planes: 64-65 turn history, 253-256 recency
 constexpr int CT0_S = 64 * NC, CT0_E = 66 * NC, CT1_S = 253 * NC, CT1_E = 257 * NC;
@@ -49,18 +59,28 @@ constexpr int AUX_ROW = 6 * NC;
 // u8 codes of the fixed values (the decode table starts 0, 1, -1, 1/3, 2/3)
 constexpr uint8_t CODE_ONE = 1, CODE_NEG = 2, CODE_THIRD = 3, CODE_2THIRD = 4;
 
+// thread roles in the build: 0..119 one pid each, 128..159 one move-history
+// slot each, 160..166 the whole-plane seat flags
+constexpr int T_HIST = PID_STRIDE, T_FLAGS = T_HIST + HIST_LEN, T_END = T_FLAGS + 7;
+
 struct ObsLds {
     alignas(16) uint32_t bits[OBS_BITS_WORDS];
     alignas(16) uint8_t img[IMG_BYTES];
+    alignas(16) uint32_t stat[STAT_NQ * 4];   // board_static words of `bits` (row-independent)
     float rec[PID_STRIDE][4];        // recency values per pid (0 unless an enemy piece on board)
     float dec[32];                   // code -> f32
     uint32_t decb[32];               // code -> bf16 bits
+    int32_t hist[HIST_LEN];          // move-history ring as stored
+    int32_t hmeta;
     int8_t cpid[CELL_STRIDE];        // canonical cell -> pid (-1 empty)
+    int8_t ptype[PID_STRIDE];        // piece type per pid
+    uint8_t bval[BC_COUNT * 12 + 4]; // belief row code x type -> value code
     float turnv[2];
 };
 
-// Byte-image address of element e of range r for a row whose first element sits
-// at element phase m (row address / element size, mod 16 / element size).
+// Byte-image address of element e of the range starting at `start` (image base
+// `base`) for a row whose first element sits at element phase m (row address /
+// element size, mod 16 / element size).
 __device__ __forceinline__ int img_off(int base, int start, int e, int m)
 {
     return base + 16 + ((start + m) & 15) + (e - start);
@@ -74,23 +94,6 @@ __device__ __forceinline__ bool img_range(int e, int &base, int &start)
     if (e >= RG2_S && e < RG2_E) { base = RG2_B; start = RG2_S; return true; }
     if (e >= RG3_S && e < RG3_E) { base = RG3_B; start = RG3_S; return true; }
     return false;
-}
-
-// Image range overlapping elements [e, e + len) (len <= 16); false if none.
-__device__ __forceinline__ bool img_overlap(int e, int len, int &base, int &start)
-{
-    const int f = e + len;
-    if (e < RG0_E && f > RG0_S) { base = RG0_B; start = RG0_S; return true; }
-    if (e < RG1_E && f > RG1_S) { base = RG1_B; start = RG1_S; return true; }
-    if (e < RG2_E && f > RG2_S) { base = RG2_B; start = RG2_S; return true; }
-    if (e < RG3_E && f > RG3_S) { base = RG3_B; start = RG3_S; return true; }
-    return false;
-}
-
-__device__ __forceinline__ bool cont_overlap(int e, int len)
-{
-    const int f = e + len;
-    return (e < CT0_E && f > CT0_S) || (e < CT1_E && f > CT1_S);
 }
 
 __device__ __forceinline__ bool back_two(int seat, int zero)
@@ -119,41 +122,90 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
     return (uint16_t)(u >> 16);
 }
 
-// Stage 1 for one pid: every nonzero element the piece contributes, scattered
-// into bits / img (observation.py:908-1620 per-piece writers).
-__device__ void obs_scatter_piece(const State &S, int env, int obs, int pid, int m, ObsLds &L)
+// Bits [base, base + 30) of the 120-bit pid set (hi:lo), i.e. the 30 pids of one seat.
+__device__ __forceinline__ uint32_t seat_bits(uint64_t lo, uint64_t hi, int base)
 {
-    const int tm = (obs + 2) & 3, le = (obs + 1) & 3, re = (obs + 3) & 3, team = obs & 1;
+    const uint64_t w = base == 0 ? lo : base < 64 ? ((lo >> base) | (hi << (64 - base))) : (hi >> (base - 64));
+    return (uint32_t)w & 0x3FFFFFFFu;
+}
+
+// World flat cell -> canonical flat cell of observer s (rotation.py:44-85).
+__device__ __forceinline__ int canon_cell(int s, int f)
+{
+    const int x = f % 17, y = f / 17;
+    const int cx = s == 0 ? x : s == 1 ? y : s == 2 ? 16 - x : 16 - y;
+    const int cy = s == 0 ? y : s == 1 ? 16 - x : s == 2 ? 16 - y : x;
+    return cy * 17 + cx;
+}
+
+// Everything one pid contributes, loaded in one batch of independent reads
+// before the block's first barrier (observation.py:908-1620 per-piece writers).
+struct PieceIn {
+    int pos, tp, mcount, aeat, psurv, dstep, dreason, dloc, zero, bcode;
+    uint64_t dlo, dhi, clo, chi;   // observer's combat memory (enemy pieces)
+    int dtype, ctype, ocnt, floor, flags, ldir, lchain, fstep;
+    uint64_t elo, ehi;             // eaten_by of the observer's own pieces
+    uint64_t ldlo, ldhi, rdlo, rdhi;  // left / right enemies' memory of an own piece
+    int locnt, rocnt, lflags, rflags;
+};
+
+__device__ __forceinline__ void piece_load(const State &S, int env, int obs, int pid, PieceIn &P)
+{
+    const int le = (obs + 1) & 3, re = (obs + 3) & 3, s = pid / 30;
     const size_t pi = (size_t)env * PID_STRIDE + pid;
-    const int pos = S.pos[pi];
-    const int tp = S.ptype[pi];
+    P.pos = S.pos[pi]; P.tp = S.ptype[pi];
+    P.mcount = S.mcount[pi]; P.aeat = S.aeat[pi]; P.psurv = S.psurv[pi];
+    P.dstep = S.dstep[pi]; P.dreason = S.dreason[pi]; P.dloc = S.dloc[pi]; P.zero = S.zero[pi];
+    P.bcode = S.bcode[((size_t)env * 4 + obs) * PID_STRIDE + pid];
+    const size_t ci = cm_idx(env, obs, pid);
+    P.dlo = P.dhi = P.clo = P.chi = P.elo = P.ehi = P.ldlo = P.ldhi = P.rdlo = P.rdhi = 0;
+    P.dtype = P.ctype = P.ocnt = P.floor = P.flags = 0;
+    P.ldir = P.lchain = P.fstep = -1;
+    P.locnt = P.rocnt = P.lflags = P.rflags = 0;
+    if ((s & 1) != (obs & 1)) {
+        P.dlo = S.cm_dlo[ci]; P.dhi = S.cm_dhi[ci]; P.clo = S.cm_clo[ci]; P.chi = S.cm_chi[ci];
+        P.dtype = S.cm_dtype[ci]; P.ctype = S.cm_ctype[ci]; P.ocnt = S.cm_ocnt[ci];
+        P.floor = S.cm_floor[ci]; P.flags = S.cm_flags[ci];
+        P.ldir = S.cm_ldir[ci]; P.lchain = S.cm_lchain[ci]; P.fstep = S.cm_fstep[ci];
+    } else if (s == obs) {
+        P.elo = S.cm_elo[ci]; P.ehi = S.cm_ehi[ci];
+        const size_t li = cm_idx(env, le, pid), ri = cm_idx(env, re, pid);
+        P.ldlo = S.cm_dlo[li]; P.ldhi = S.cm_dhi[li]; P.locnt = S.cm_ocnt[li]; P.lflags = S.cm_flags[li];
+        P.rdlo = S.cm_dlo[ri]; P.rdhi = S.cm_dhi[ri]; P.rocnt = S.cm_ocnt[ri]; P.rflags = S.cm_flags[ri];
+    }
+}
+
+// Scatter one pid's nonzero elements into bits / img.
+__device__ void piece_scatter(const State &S, int obs, int pid, int m, const PieceIn &P, const float rc[4], ObsLds &L)
+{
+    const int tm = (obs + 2) & 3, le = (obs + 1) & 3, team = obs & 1;
     const int s = pid / 30;
     const int rel = s == obs ? 0 : s == tm ? 1 : s == le ? 2 : 3;
     const bool ours = (s & 1) == team;
-    float rc[4] = {0.f, 0.f, 0.f, 0.f};
 
-    if ((unsigned)pos < (unsigned)NC) {
-        const int k = cT.rot[obs][pos];
+    if ((unsigned)P.pos < (unsigned)NC) {
+        const int k = canon_cell(obs, P.pos);
+        L.cpid[k] = (int8_t)pid;
         // piece_own (0-11), side occupancy (25, 26), dark_teammate (24)
-        if (rel == 0 && tp >= 2 && tp <= 13) set_el(L, (tp - 2) * NC + k);
+        if (rel == 0 && P.tp >= 2 && P.tp <= 13) set_el(L, (P.tp - 2) * NC + k);
         if (rel == 2) set_el(L, 25 * NC + k);
         if (rel == 3) set_el(L, 26 * NC + k);
         if (rel == 1 && S.show_mode == SM_DARK) set_el(L, 24 * NC + k);
         // beliefs (12-23 teammate, 27-38 left, 39-50 right)
         if (rel != 0) {
-            int bc = S.bcode[((size_t)env * 4 + obs) * PID_STRIDE + pid];
-            bc = bc < BC_COUNT ? bc : 0;
+            const int bc = P.bcode < BC_COUNT ? P.bcode : 0;
             const int c0 = rel == 1 ? 12 : rel == 2 ? 27 : 39;
             const int base = rel == 1 ? RG0_B : RG1_B, start = rel == 1 ? RG0_S : RG1_S;
+#pragma unroll 1
             for (int j = 0; j < 12; ++j) {
-                const uint8_t v = cBVAL[bc][j];
+                const uint8_t v = L.bval[bc * 12 + j];
                 if (v) set_code(L, base, start, (c0 + j) * NC + k, m, v);
             }
         }
         // move / active_eat / passive_survive buckets (66-89): own team in the
         // first four planes of each group, the other team in the last four
         const int half = ours ? 0 : 4;
-        const int mb = min((int)S.mcount[pi], 3), eb = min((int)S.aeat[pi], 3), sb = min((int)S.psurv[pi], 3);
+        const int mb = min(P.mcount, 3), eb = min(P.aeat, 3), sb = min(P.psurv, 3);
         set_el(L, (66 + half + mb) * NC + k);
         for (int q = 0; q <= eb; ++q) set_el(L, (74 + half + q) * NC + k);
         for (int q = 0; q <= sb; ++q) set_el(L, (82 + half + q) * NC + k);
@@ -163,62 +215,42 @@ __device__ void obs_scatter_piece(const State &S, int env, int obs, int pid, int
 
         uint64_t cmb = 0;
         if (!ours) {   // combat-memory layers 1 and 3 (observation.py:1292-1387, 1475-1567)
-            const size_t ci = cm_idx(env, obs, pid);
-            const uint64_t dlo = S.cm_dlo[ci], dhi = S.cm_dhi[ci];
-            const int mcnt = __popcll(dlo) + __popcll(dhi);
-            const int ocnt = S.cm_ocnt[ci];
-            const int ccnt = __popcll(S.cm_clo[ci]) + __popcll(S.cm_chi[ci]);
-            const int fl = S.cm_floor[ci];
-            const uint8_t flg = S.cm_flags[ci];
-            cmb |= (uint64_t)(S.cm_dtype[ci] & 0xFFF);
+            const int mcnt = __popcll(P.dlo) + __popcll(P.dhi);
+            const int ccnt = __popcll(P.clo) + __popcll(P.chi);
+            cmb |= (uint64_t)(P.dtype & 0xFFF);
             for (int q = 0; q < 3; ++q) {
                 if (mcnt >= q + 1) cmb |= 1ull << (12 + q);
-                if (ocnt >= q + 1) cmb |= 1ull << (15 + q);
+                if (P.ocnt >= q + 1) cmb |= 1ull << (15 + q);
                 if (ccnt >= q + 1) cmb |= 1ull << (30 + q);
             }
-            cmb |= (uint64_t)(S.cm_ctype[ci] & 0xFFF) << 18;
-            for (int q = 0; q < 9; ++q) if (fl >= q + 1) cmb |= 1ull << (33 + q);
-            if (flg & CMF_IS_GONGB) cmb |= 1ull << 42;
-            if (flg & CMF_NOT_GONGB) cmb |= 1ull << 43;
-            if (back_two(s, S.zero[pi]) && S.mcount[pi] == 0 && !(flg & CMF_ATK_GONGB)) cmb |= 1ull << 44;
+            cmb |= (uint64_t)(P.ctype & 0xFFF) << 18;
+            for (int q = 0; q < 9; ++q) if (P.floor >= q + 1) cmb |= 1ull << (33 + q);
+            if (P.flags & CMF_IS_GONGB) cmb |= 1ull << 42;
+            if (P.flags & CMF_NOT_GONGB) cmb |= 1ull << 43;
+            if (back_two(s, P.zero) && P.mcount == 0 && !(P.flags & CMF_ATK_GONGB)) cmb |= 1ull << 44;
             // kill_mine_slot (223-252) and kill_mine_count (211-222) over the
             // observer's own pieces this one has killed directly
             uint64_t tcnt = 0;   // 12 counters of 5 bits, one per tracked type
-            for (int sl = 0; sl < 30; ++sl) {
-                const int gp = obs * 30 + sl;
-                const bool hit = gp < 64 ? ((dlo >> gp) & 1) : ((dhi >> (gp - 64)) & 1);
-                if (!hit) continue;
+            for (uint32_t hits = seat_bits(P.dlo, P.dhi, obs * 30); hits; hits &= hits - 1) {
+                const int sl = __builtin_ctz(hits);
                 set_el(L, (223 + sl) * NC + k);
-                const int gt = S.ptype[(size_t)env * PID_STRIDE + gp];
+                const int gt = L.ptype[obs * 30 + sl];
                 if (gt >= 2 && gt <= 13) tcnt += 1ull << (5 * (gt - 2));
             }
+#pragma unroll 1
             for (int q = 0; q < 12; ++q) {
                 const int c = (int)((tcnt >> (5 * q)) & 31u);
                 if (c) set_code(L, RG3_B, RG3_S, (211 + q) * NC + k, m,
                                 c == 1 ? CODE_THIRD : c == 2 ? CODE_2THIRD : CODE_ONE);
             }
-            const int mc = S.mc[env];
-            const int ldir = S.cm_ldir[ci], lchain = S.cm_lchain[ci], fstep = S.cm_fstep[ci];
-            auto recency = [&](int last, int q) {
-                if (last < 0) return 0.f;
-                int el = mc - last;
-                el = el < 0 ? 0 : (el > 4095 ? 4095 : el);
-                return S.rlut[q * 4096 + el];
-            };
-            rc[0] = recency(ldir, 0);
-            rc[1] = recency(ldir, 1);
-            rc[2] = recency(lchain, 2);
-            rc[3] = recency(fstep, 3);
         } else if (s == obs) {   // layer 2 (observation.py:1392-1451)
-            const size_t li = cm_idx(env, le, pid), ri = cm_idx(env, re, pid);
-            const int lc = __popcll(S.cm_dlo[li]) + __popcll(S.cm_dhi[li]) + S.cm_ocnt[li];
-            const int rcnt = __popcll(S.cm_dlo[ri]) + __popcll(S.cm_dhi[ri]) + S.cm_ocnt[ri];
+            const int lc = __popcll(P.ldlo) + __popcll(P.ldhi) + P.locnt;
+            const int rcnt = __popcll(P.rdlo) + __popcll(P.rdhi) + P.rocnt;
             const int pk = lc < rcnt ? lc : rcnt;
             for (int q = 0; q < 3; ++q) if (pk >= q + 1) cmb |= 1ull << (45 + q);
-            const uint8_t lf = S.cm_flags[li], rf = S.cm_flags[ri];
-            if ((lf & CMF_IS_GONGB) && (rf & CMF_IS_GONGB)) cmb |= 1ull << 48;
-            const bool atk = (lf & CMF_ATK_GONGB) || (rf & CMF_ATK_GONGB);
-            if (back_two(s, S.zero[pi]) && S.mcount[pi] == 0 && !atk) cmb |= 1ull << 49;
+            if ((P.lflags & CMF_IS_GONGB) && (P.rflags & CMF_IS_GONGB)) cmb |= 1ull << 48;
+            const bool atk = (P.lflags & CMF_ATK_GONGB) || (P.rflags & CMF_ATK_GONGB);
+            if (back_two(s, P.zero) && P.mcount == 0 && !atk) cmb |= 1ull << 49;
         }
         while (cmb) {   // combat-memory bit planes 161-210
             const int b = __builtin_ctzll(cmb);
@@ -229,91 +261,160 @@ __device__ void obs_scatter_piece(const State &S, int env, int obs, int pid, int
     for (int q = 0; q < 4; ++q) L.rec[pid][q] = rc[q];
 
     // death_reason (90-101) and dead_at_zero (102-103), observation.py:1103-1180
-    const int dstp = S.dstep[pi];
-    if (dstp >= 0) {
-        const int reason = S.dreason[pi], loc = S.dloc[pi], z = S.zero[pi];
+    if (P.dstep >= 0) {
         const int grp = rel == 0 ? 0 : rel == 1 ? 3 : rel == 2 ? 6 : 9;
-        if (reason >= 0 && reason <= 2 && dstp > 0 && (unsigned)loc < (unsigned)NC)
-            set_el(L, (90 + grp + reason) * NC + cT.rot[obs][loc]);
-        if ((unsigned)z < (unsigned)NC) set_el(L, (102 + (ours ? 0 : 1)) * NC + cT.rot[obs][z]);
+        if (P.dreason >= 0 && P.dreason <= 2 && P.dstep > 0 && (unsigned)P.dloc < (unsigned)NC)
+            set_el(L, (90 + grp + P.dreason) * NC + canon_cell(obs, P.dloc));
+        if ((unsigned)P.zero < (unsigned)NC) set_el(L, (102 + (ours ? 0 : 1)) * NC + canon_cell(obs, P.zero));
     }
     // eaten_by_pid (257-316), layer 4 (observation.py:1591-1620): the observer's
     // own piece, at its cell or (dead) its zero cell, marks its killers
     if (rel == 0) {
-        const int cell = pos >= 0 ? pos : S.zero[pi];
+        const int cell = P.pos >= 0 ? P.pos : P.zero;
         if ((unsigned)cell < (unsigned)NC) {
-            const size_t ci = cm_idx(env, obs, pid);
-            const uint64_t elo = S.cm_elo[ci], ehi = S.cm_ehi[ci];
-            const int k = cT.rot[obs][cell];
-            for (int half = 0; half < 2; ++half) {
-                const int opp = half == 0 ? le : re;
-                for (int sl = 0; sl < 30; ++sl) {
-                    const int gp = opp * 30 + sl;
-                    const bool hit = gp < 64 ? ((elo >> gp) & 1) : ((ehi >> (gp - 64)) & 1);
-                    if (hit) set_el(L, (257 + half * 30 + sl) * NC + k);
-                }
-            }
+            const int k = canon_cell(obs, cell);
+            const int re = (obs + 3) & 3;
+            uint64_t hits = (uint64_t)seat_bits(P.elo, P.ehi, le * 30) | ((uint64_t)seat_bits(P.elo, P.ehi, re * 30) << 30);
+            for (; hits; hits &= hits - 1) set_el(L, (257 + __builtin_ctzll(hits)) * NC + k);
         }
     }
 }
 
-// Build the LDS form of row (env, obs); m is the row's element phase.
-__device__ void obs_build(const State &S, int env, int obs, int m, ObsLds &L)
+
+// One thread's inputs of a row, loaded ahead of the build that uses them.
+struct RowIn {
+    PieceIn P;      // t < NP
+    int ptype;      // t < PID_STRIDE
+    int hist, hmeta;  // T_HIST <= t < T_FLAGS: ring slot t - T_HIST
+    int flag_on;    // T_FLAGS <= t < T_END
+    int mc, mslc;
+    float gval;     // t < 28: the row's global feature t
+};
+
+__device__ __forceinline__ int row_env(int row, int all_seats) { return all_seats ? row >> 2 : row; }
+
+__device__ __forceinline__ int row_obs(const State &S, const int8_t *observer, int all_seats, int row)
+{
+    if (all_seats) return row & 3;
+    const int env = row;
+    return (observer ? observer[env] : S.turn[env]) & 3;
+}
+
+// Seat of the observer's i-th relation in plane order: self, teammate, left, right.
+__device__ __forceinline__ int seat_rel(int obs, int i) { return (obs + (i == 0 ? 0 : i == 1 ? 2 : i == 2 ? 1 : 3)) & 3; }
+
+__device__ void row_load(const State &S, int env, int obs, int t, RowIn &R)
+{
+    R.mc = S.mc[env];
+    R.mslc = S.mslc[env];
+    R.ptype = t < PID_STRIDE ? S.ptype[(size_t)env * PID_STRIDE + t] : -1;
+    R.hist = 0; R.hmeta = 0; R.flag_on = 0;
+    if (t < NP) {
+        piece_load(S, env, obs, t, R.P);
+    } else if (t >= T_HIST && t < T_FLAGS) {
+        R.hist = S.hist[(size_t)env * HIST_LEN + (t - T_HIST)];
+        R.hmeta = S.hmeta[env];
+    } else if (t >= T_FLAGS && t < T_END) {
+        const int j = t - T_FLAGS;
+        R.flag_on = j < 3 ? ((S.sdead[env] >> seat_rel(obs, j + 1)) & 1) : ((S.sflag[env] >> seat_rel(obs, j - 3)) & 1);
+    }
+    R.gval = 0.f;
+    if (t < 24) {   // remaining counts of the left / right enemy (observation.py:1623-1651)
+        const int seat = t < 12 ? (obs + 1) & 3 : (obs + 3) & 3;
+        const bool trk = (S.remtrk[(size_t)env * 4 + obs] >> seat) & 1;
+        const int cnt = S.rem[((size_t)env * 4 + obs) * 48 + seat * 12 + t % 12];
+        R.gval = trk ? (float)cnt : 0.f;
+    } else if (t < 28) {   // flag_revealed of self, teammate, left, right
+        R.gval = (float)((S.sflag[env] >> seat_rel(obs, t - 24)) & 1);
+    }
+}
+
+// Row-independent LDS content, once per block.
+__device__ void obs_setup(ObsLds &L)
 {
     const int t = threadIdx.x;
-    {
-        uint4 *w = reinterpret_cast<uint4 *>(L.bits);
-        for (int i = t; i < OBS_BITS_WORDS / 4; i += OBS_THREADS) w[i] = make_uint4(0, 0, 0, 0);
-        uint4 *b = reinterpret_cast<uint4 *>(L.img);
-        for (int i = t; i < IMG_BYTES / 16; i += OBS_THREADS) b[i] = make_uint4(0, 0, 0, 0);
-    }
-    const int8_t *cellg = S.cell + (size_t)env * CELL_STRIDE;
-    for (int k = t; k < CELL_STRIDE; k += OBS_THREADS) L.cpid[k] = k < NC ? cellg[cT.unrot[obs][k]] : (int8_t)-1;
+    for (int i = t; i < BC_COUNT * 12; i += OBS_THREADS) L.bval[i] = cBVAL[i / 12][i % 12];
     if (t < 32) {
         const float d = t < 17 ? cDECODE[t] : 0.f;
         L.dec[t] = d;
         L.decb[t] = f32_to_bf16_rne(d);
     }
+    if (t < STAT_NQ * 4) L.stat[t] = 0;
+    __syncthreads();
+    for (int k = t; k < NC; k += OBS_THREADS) {   // board_static (58-63): fixed cell classes
+        uint32_t sm = cT.statics[k];
+        while (sm) {
+            const int b = __builtin_ctz(sm);
+            sm &= sm - 1;
+            if (b < 6) {
+                const int e = (58 + b) * NC + k;
+                atomicOr(&L.stat[(e >> 5) - STAT_Q0 * 4], 1u << (e & 31));
+            }
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ float recency_at(const State &S, int mc, int last, int q)
+{   // exp(-elapsed / tau) from the table (observation.py:1545-1567)
+    if (last < 0) return 0.f;
+    int el = mc - last;
+    el = el < 0 ? 0 : (el > 4095 ? 4095 : el);
+    return S.rlut[q * 4096 + el];
+}
+
+// Build the LDS form of row (env, obs) from R; m is the row's element phase.
+__device__ void obs_build(const State &S, int obs, int m, const RowIn &R, ObsLds &L)
+{
+    const int t = threadIdx.x;
+    float rc[4] = {0.f, 0.f, 0.f, 0.f};   // gathered first: the latency overlaps the clears
+    if (t < NP && (unsigned)R.P.pos < (unsigned)NC && ((t / 30) & 1) != (obs & 1)) {
+        rc[0] = recency_at(S, R.mc, R.P.ldir, 0);
+        rc[1] = recency_at(S, R.mc, R.P.ldir, 1);
+        rc[2] = recency_at(S, R.mc, R.P.lchain, 2);
+        rc[3] = recency_at(S, R.mc, R.P.fstep, 3);
+    }
+    {
+        uint4 *w = reinterpret_cast<uint4 *>(L.bits);
+        const uint4 *st = reinterpret_cast<const uint4 *>(L.stat);
+        for (int i = t; i < OBS_BITS_WORDS / 4; i += OBS_THREADS)
+            w[i] = (unsigned)(i - STAT_Q0) < (unsigned)STAT_NQ ? st[i - STAT_Q0] : make_uint4(0, 0, 0, 0);
+        uint4 *b = reinterpret_cast<uint4 *>(L.img);
+        for (int i = t; i < IMG_BYTES / 16; i += OBS_THREADS) b[i] = make_uint4(0, 0, 0, 0);
+    }
+    for (int k = t; k < CELL_STRIDE; k += OBS_THREADS) L.cpid[k] = -1;
+    if (t < PID_STRIDE) L.ptype[t] = (int8_t)R.ptype;
+    if (t >= T_HIST && t < T_FLAGS) {
+        L.hist[t - T_HIST] = R.hist;
+        if (t == T_HIST) L.hmeta = R.hmeta;
+    }
     if (t == 0) {   // turn_history: float64 divide, then rounded to float32 (observation.py:1000-1021)
-        double dp = (double)S.mslc[env] / 200.0; if (dp > 1.0) dp = 1.0;
-        double mp = (double)S.mc[env] / 4000.0; if (mp > 1.0) mp = 1.0;
+        double dp = (double)R.mslc / 200.0; if (dp > 1.0) dp = 1.0;
+        double mp = (double)R.mc / 4000.0; if (mp > 1.0) mp = 1.0;
         L.turnv[0] = (float)dp; L.turnv[1] = (float)mp;
     }
     __syncthreads();
-    if (t < PID_STRIDE) {
-        if (t < NP) obs_scatter_piece(S, env, obs, t, m, L);
-        else for (int q = 0; q < 4; ++q) L.rec[t][q] = 0.f;
-    } else if (t < PID_STRIDE + HIST_LEN) {   // move_history (129-160), observation.py:1207-1231
-        const int d = t - PID_STRIDE;
-        const int meta = S.hmeta[env];
-        const int cnt = meta & 0xFF, head = (meta >> 8) & 31;
+    if (t < NP) {
+        piece_scatter(S, obs, t, m, R.P, rc, L);
+    } else if (t < PID_STRIDE) {
+        for (int q = 0; q < 4; ++q) L.rec[t][q] = 0.f;
+    } else if (t < T_FLAGS) {   // move_history (129-160), observation.py:1207-1231
+        const int d = t - T_HIST;
+        const int cnt = L.hmeta & 0xFF, head = (L.hmeta >> 8) & 31;
         if (d < cnt) {
-            const int e = S.hist[(size_t)env * HIST_LEN + ((head - 1 - d) & 31)];
-            const int hs = cT.rot[obs][min(e & 0xFFFF, NC - 1)];
-            const int hd = cT.rot[obs][min((e >> 16) & 0xFFFF, NC - 1)];
+            const int e = L.hist[(head - 1 - d) & 31];
+            const int hs = canon_cell(obs, min(e & 0xFFFF, NC - 1));
+            const int hd = canon_cell(obs, min((e >> 16) & 0xFFFF, NC - 1));
             if (hs != hd) set_code(L, RG2_B, RG2_S, (129 + d) * NC + hs, m, CODE_NEG);
             set_code(L, RG2_B, RG2_S, (129 + d) * NC + hd, m, CODE_ONE);
         }
-    } else if (t < PID_STRIDE + HIST_LEN + 7) {   // whole planes: dead_flags 51-53, flag_revealed 54-57
-        const int j = t - PID_STRIDE - HIST_LEN;
-        // seats in plane order: self, teammate, left enemy, right enemy
-        auto seat_at = [&](int i) { return (obs + (i == 0 ? 0 : i == 1 ? 2 : i == 2 ? 1 : 3)) & 3; };
-        const bool on = j < 3 ? ((S.sdead[env] >> seat_at(j + 1)) & 1) : ((S.sflag[env] >> seat_at(j - 3)) & 1);
-        if (on) {
-            const int e0 = (51 + j) * NC, e1 = e0 + NC;
+    } else if (t < T_END) {   // whole planes: dead_flags 51-53, flag_revealed 54-57
+        if (R.flag_on) {
+            const int e0 = (51 + t - T_FLAGS) * NC, e1 = e0 + NC;
             for (int w = e0 >> 5; w <= (e1 - 1) >> 5; ++w) {
                 const int lo = max(e0, w * 32) - w * 32, hi = min(e1, w * 32 + 32) - w * 32;
                 const uint32_t mask = (hi - lo == 32) ? 0xFFFFFFFFu : (((1u << (hi - lo)) - 1u) << lo);
                 atomicOr(&L.bits[w], mask);
-            }
-        }
-    } else {   // board_static (58-63): fixed cell classes of the canonical frame
-        for (int k = t - (PID_STRIDE + HIST_LEN + 7); k < NC; k += OBS_THREADS - (PID_STRIDE + HIST_LEN + 7)) {
-            uint32_t sm = cT.statics[k];
-            while (sm) {
-                const int b = __builtin_ctz(sm);
-                sm &= sm - 1;
-                if (b < 6) set_el(L, (58 + b) * NC + k);
             }
         }
     }
@@ -361,73 +462,104 @@ __device__ __forceinline__ uint32_t nib_to_bytes(uint32_t nib)
     return __umul24(nib & 0xFu, 0x00204081u) & 0x01010101u;
 }
 
-// Stream the 91,613-element row to `row` (element size ES, 16-byte chunks).
+// One full 16-byte chunk whose first element is e0. `off` is the image offset
+// of e0 (IMG_ZERO when the chunk touches no image range).
+template <int FMT>
+__device__ __forceinline__ uint4 obs_chunk(const ObsLds &L, int e0, int off, bool img)
+{
+    const uint32_t v = bit_window(L, e0);
+    uint32_t w[4];
+    if (FMT == 2) {
+        for (int i = 0; i < 4; ++i) w[i] = nib_to_bytes(v >> (4 * i));
+        if (img) {
+            const uint4 b = *reinterpret_cast<const uint4 *>(&L.img[off]);
+            w[0] |= b.x; w[1] |= b.y; w[2] |= b.z; w[3] |= b.w;
+        }
+    } else if (FMT == 1) {
+        if (img) {
+            const uint2 b = *reinterpret_cast<const uint2 *>(&L.img[off]);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t cw = i < 2 ? b.x : b.y;
+                const int sh = (i & 1) * 16;
+                const uint32_t c0 = ((cw >> sh) & 0xFFu) | ((v >> (2 * i)) & 1u);
+                const uint32_t c1 = ((cw >> (sh + 8)) & 0xFFu) | ((v >> (2 * i + 1)) & 1u);
+                w[i] = L.decb[c0] | (L.decb[c1] << 16);
+            }
+        } else {
+            for (int i = 0; i < 4; ++i)
+                w[i] = (((v >> (2 * i)) & 1u) ? 0x3F80u : 0u) | (((v >> (2 * i + 1)) & 1u) ? 0x3F800000u : 0u);
+        }
+    } else {
+        if (img) {
+            const uint32_t cw = *reinterpret_cast<const uint32_t *>(&L.img[off]);
+            for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(L.dec[((cw >> (8 * i)) & 0xFFu) | ((v >> i) & 1u)]);
+        } else {
+            for (int i = 0; i < 4; ++i) w[i] = ((v >> i) & 1u) ? 0x3F800000u : 0u;
+        }
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Elements [e, f) of the row written one by one (row ends, continuous planes).
+template <int FMT>
+__device__ void obs_elems(const ObsLds &L, uint8_t *row, int e, int f, int m)
+{
+    for (; e < f; ++e) {
+        const uint32_t v = obs_elem<FMT>(L, e, m);
+        if (FMT == 2) row[e] = (uint8_t)v;
+        else if (FMT == 1) reinterpret_cast<uint16_t *>(row)[e] = (uint16_t)v;
+        else reinterpret_cast<uint32_t *>(row)[e] = v;
+    }
+}
+
+// Stream the 91,613-element row to `row` (element phase m) in 16-byte chunks:
+// chunk q covers row bytes [16q - lead, 16q - lead + 16).
 template <int FMT>
 __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m)
 {
     constexpr int ES = FMT == 0 ? 4 : FMT == 1 ? 2 : 1;
     constexpr int EPC = 16 / ES;
-    const uintptr_t B = (uintptr_t)row;
-    const uintptr_t A0 = B & ~(uintptr_t)15;
-    const uintptr_t E = B + (uintptr_t)OBS_ROW * ES;
-    const int nchunks = (int)((E - A0 + 15) >> 4);
-    for (int q = threadIdx.x; q < nchunks; q += OBS_THREADS) {
-        const uintptr_t A = A0 + (uintptr_t)q * 16;
-        if (A < B || A + 16 > E) {   // partial chunk at either end of the row
-            const uintptr_t lo = A < B ? B : A, hi = A + 16 > E ? E : A + 16;
-            for (uintptr_t p = lo; p < hi; p += ES) {
-                const int e = (int)((p - B) / ES);
-                const uint32_t v = obs_elem<FMT>(L, e, m);
-                if (ES == 1) *reinterpret_cast<uint8_t *>(p) = (uint8_t)v;
-                else if (ES == 2) *reinterpret_cast<uint16_t *>(p) = (uint16_t)v;
-                else *reinterpret_cast<uint32_t *>(p) = v;
-            }
+    constexpr int NBYTES = OBS_ROW * ES;
+    const int lead = m * ES;
+    const int qf = lead ? 1 : 0, ql = (NBYTES + lead) >> 4;   // full chunks [qf, ql)
+    const int d0 = RG0_B + 16 + ((RG0_S + m) & 15) - RG0_S, d1 = RG1_B + 16 + ((RG1_S + m) & 15) - RG1_S;
+    const int d2 = RG2_B + 16 + ((RG2_S + m) & 15) - RG2_S, d3 = RG3_B + 16 + ((RG3_S + m) & 15) - RG3_S;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    for (int qb = qf + wv * 64; qb < ql; qb += OBS_THREADS) {
+        // the wave's span: chunk starts s_lo .. s_hi - EPC (uniform)
+        const int s_lo = qb * EPC - m, s_hi = min(qb + 64, ql) * EPC - m;
+        const int q = qb + lane;
+        const int e0 = q * EPC - m;
+        uint8_t *dst = row + (ptrdiff_t)e0 * ES;
+        if (FMT != 2 && ((s_lo < CT0_E && s_hi > CT0_S) || (s_lo < CT1_E && s_hi > CT1_S))) {
+            if (q < ql) obs_elems<FMT>(L, row, e0, e0 + EPC, m);
             continue;
         }
-        const int e0 = (int)((A - B) / ES);
-        uint32_t w[4];
-        if (FMT != 2 && cont_overlap(e0, EPC)) {
-            for (int i = 0; i < 4; ++i) w[i] = 0;
-            for (int i = 0; i < EPC; ++i) {
-                const uint32_t v = obs_elem<FMT>(L, e0 + i, m);
-                w[(i * ES) >> 2] |= v << (((i * ES) & 3) * 8);
-            }
+        int nov = 0, d = 0, rs = 0, re = 0;
+        if (s_lo < RG0_E && s_hi > RG0_S) { ++nov; d = d0; rs = RG0_S; re = RG0_E; }
+        if (s_lo < RG1_E && s_hi > RG1_S) { ++nov; d = d1; rs = RG1_S; re = RG1_E; }
+        if (s_lo < RG2_E && s_hi > RG2_S) { ++nov; d = d2; rs = RG2_S; re = RG2_E; }
+        if (s_lo < RG3_E && s_hi > RG3_S) { ++nov; d = d3; rs = RG3_S; re = RG3_E; }
+        if (q >= ql) continue;
+        uint4 out;
+        if (nov == 0) {
+            out = obs_chunk<FMT>(L, e0, IMG_ZERO, false);
+        } else if (nov == 1 && s_lo >= rs - 16 && s_hi - EPC <= re) {
+            out = obs_chunk<FMT>(L, e0, e0 + d, true);   // every chunk reads inside range's margins
         } else {
-            const uint32_t v = bit_window(L, e0);
-            int base, start;
-            const bool ov = img_overlap(e0, EPC, base, start);
-            if (FMT == 2) {
-                for (int i = 0; i < 4; ++i) w[i] = nib_to_bytes(v >> (4 * i));
-                if (ov) {
-                    const uint4 b = *reinterpret_cast<const uint4 *>(&L.img[img_off(base, start, e0, m)]);
-                    w[0] |= b.x; w[1] |= b.y; w[2] |= b.z; w[3] |= b.w;
-                }
-            } else if (FMT == 1) {
-                if (ov) {
-                    const uint2 b = *reinterpret_cast<const uint2 *>(&L.img[img_off(base, start, e0, m)]);
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t cw = i < 2 ? b.x : b.y;
-                        const int sh = (i & 1) * 16;
-                        const uint32_t c0 = ((cw >> sh) & 0xFFu) | ((v >> (2 * i)) & 1u);
-                        const uint32_t c1 = ((cw >> (sh + 8)) & 0xFFu) | ((v >> (2 * i + 1)) & 1u);
-                        w[i] = L.decb[c0] | (L.decb[c1] << 16);
-                    }
-                } else {
-                    for (int i = 0; i < 4; ++i)
-                        w[i] = ((v >> (2 * i)) & 1u) * 0x3F80u + ((v >> (2 * i + 1)) & 1u) * 0x3F800000u;
-                }
-            } else {
-                if (ov) {
-                    const uint32_t cw = *reinterpret_cast<const uint32_t *>(&L.img[img_off(base, start, e0, m)]);
-                    for (int i = 0; i < 4; ++i)
-                        w[i] = __float_as_uint(L.dec[((cw >> (8 * i)) & 0xFFu) | ((v >> i) & 1u)]);
-                } else {
-                    for (int i = 0; i < 4; ++i) w[i] = ((v >> i) & 1u) * 0x3F800000u;
-                }
-            }
+            int off = IMG_ZERO;
+            if (e0 < RG0_E && e0 + EPC > RG0_S) off = e0 + d0;
+            if (e0 < RG1_E && e0 + EPC > RG1_S) off = e0 + d1;
+            if (e0 < RG2_E && e0 + EPC > RG2_S) off = e0 + d2;
+            if (e0 < RG3_E && e0 + EPC > RG3_S) off = e0 + d3;
+            out = obs_chunk<FMT>(L, e0, off, true);
         }
-        *reinterpret_cast<uint4 *>(A) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint4 *>(dst) = out;
     }
+    // partial chunks at the two ends of the row
+    if (threadIdx.x == 0 && lead) obs_elems<FMT>(L, row, 0, EPC - m, m);
+    if (threadIdx.x == 64 && ((NBYTES + lead) & 15)) obs_elems<FMT>(L, row, ql * EPC - m, OBS_ROW, m);
 }
 
 // The six continuous planes of the u8 format as float32 (N, 6, 17, 17).
@@ -446,41 +578,52 @@ __device__ void obs_emit_aux(const ObsLds &L, float *row)
             const int j = e / NC, k = e - j * NC;
             w[(p - A) >> 2] = __float_as_uint(obs_cont_at(L, j < 2 ? 64 + j : 251 + j, k));
         }
-        if (lo == A && hi == A + 16) *reinterpret_cast<uint4 *>(A) = make_uint4(w[0], w[1], w[2], w[3]);
-        else for (uintptr_t p = lo; p < hi; p += 4) *reinterpret_cast<uint32_t *>(p) = w[(p - A) >> 2];
+        if (lo == A && hi == A + 16)
+            *reinterpret_cast<uint4 *>(row + (ptrdiff_t)(A - B) / 4) = make_uint4(w[0], w[1], w[2], w[3]);
+        else
+            for (uintptr_t p = lo; p < hi; p += 4) row[(p - B) / 4] = __uint_as_float(w[(p - A) >> 2]);
     }
 }
 
+// nrows = N (one row per env, observer given or the acting seat) or 4N
+// (all_seats: row = env * 4 + observer). Launched with at most the number of
+// co-resident blocks; block b handles rows b, b + gridDim.x, ...
 template <int FMT>
-__global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *__restrict__ observer, int all_seats,
+__global__ __launch_bounds__(OBS_THREADS) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_observe(State S, const int8_t *__restrict__ observer, int all_seats,
                                                          void *__restrict__ spatial, float *__restrict__ aux,
-                                                         float *__restrict__ glob)
+                                                         float *__restrict__ glob, int nrows)
 {
     __shared__ ObsLds L;
-    const int row = blockIdx.x;
-    const int env = all_seats ? row >> 2 : row;
-    if (env >= S.n) return;
-    const int obs = all_seats ? (row & 3) : (observer ? observer[env] : S.turn[env]) & 3;
     constexpr int ES = FMT == 0 ? 4 : FMT == 1 ? 2 : 1;
-    uint8_t *rowp = reinterpret_cast<uint8_t *>(spatial) + (size_t)row * OBS_ROW * ES;
-    const int m = (int)(((uintptr_t)rowp / ES) & (16 / ES - 1));
-    obs_build(S, env, obs, m, L);
-    obs_emit<FMT>(L, rowp, m);
-    if (FMT == 2 && aux) obs_emit_aux(L, aux + (size_t)row * AUX_ROW);
-    if (glob && threadIdx.x < 28) {   // observation.py:1623-1651
-        const int t = threadIdx.x;
-        const int le = (obs + 1) & 3, re = (obs + 3) & 3;
-        float v;
-        if (t < 24) {
-            const int seat = t < 12 ? le : re, ti = t % 12;
-            const bool trk = (S.remtrk[(size_t)env * 4 + obs] >> seat) & 1;
-            v = trk ? (float)S.rem[((size_t)env * 4 + obs) * 48 + seat * 12 + ti] : 0.f;
-        } else {   // flag_revealed of self, teammate, left enemy, right enemy
-            const int i = t - 24;
-            const int seat = (obs + (i == 0 ? 0 : i == 1 ? 2 : i == 2 ? 1 : 3)) & 3;
-            v = (float)((S.sflag[env] >> seat) & 1);
+    const int t = threadIdx.x;
+    const int G = gridDim.x;
+    int row = blockIdx.x;
+    if (row >= nrows) return;
+    obs_setup(L);
+    RowIn R;
+    int obs = row_obs(S, observer, all_seats, row);
+    row_load(S, row_env(row, all_seats), obs, t, R);
+    int obs_next = row + G < nrows ? row_obs(S, observer, all_seats, row + G) : 0;
+    for (;;) {
+        uint8_t *rowp = reinterpret_cast<uint8_t *>(spatial) + (size_t)row * OBS_ROW * ES;
+        const int m = (int)(((uintptr_t)rowp / ES) & (16 / ES - 1));
+        obs_build(S, obs, m, R, L);
+        const float gv = R.gval;
+        const int nrow = row + G;
+        const bool more = nrow < nrows;
+        int obs_after = 0;
+        if (more) {   // next row's loads are in flight while this row streams out
+            row_load(S, row_env(nrow, all_seats), obs_next, t, R);
+            if (nrow + G < nrows) obs_after = row_obs(S, observer, all_seats, nrow + G);
         }
-        glob[(size_t)row * 28 + t] = v;
+        obs_emit<FMT>(L, rowp, m);
+        if (FMT == 2 && aux) obs_emit_aux(L, aux + (size_t)row * AUX_ROW);
+        if (glob && t < 28) glob[(size_t)row * 28 + t] = gv;
+        if (!more) break;
+        __syncthreads();   // the LDS row is rebuilt next
+        row = nrow;
+        obs = obs_next;
+        obs_next = obs_after;
     }
 }
 
