@@ -37,7 +37,24 @@ def parse():
     ap.add_argument("--cpu-envs", type=int, default=4096)
     ap.add_argument("--cpu-steps", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="only run a plain device copy of MB megabytes (counter calibration) and exit")
     return ap.parse_args()
+
+
+def calibrate_copy(mb: int) -> int:
+    """A plain device-to-device copy of known size, so hardware byte counters
+    (FETCH_SIZE / WRITE_SIZE) can be scaled against it."""
+    import torch
+
+    n = mb * (1 << 20)
+    a = torch.ones(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n, "launches": 3}), flush=True)
+    return 0
 
 
 def cpu_baseline(envs: int, steps: int) -> dict:
@@ -82,8 +99,22 @@ def cpu_baseline(envs: int, steps: int) -> dict:
                       f"random legal actions, HALF_DARK"}
 
 
+def measured_traffic(kernel: str, games: int):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, scaled against a
+    plain copy) from the committed counter summary, when it was taken at this size."""
+    path = ROOT / "profiles" / "traffic.json"
+    if games != 32768 or not path.exists():
+        return None
+    rec = json.loads(path.read_text()).get("kernels", {}).get(kernel)
+    if not rec:
+        return None
+    return round(rec["read_bytes"] + rec["write_bytes"])
+
+
 def main() -> int:
     args = parse()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the environment shards by games with no exchange, "
               "so runs with more than one GPU are not part of this build", file=sys.stderr)
@@ -166,7 +197,8 @@ def main() -> int:
                                f"of the acting seat, {n} games, HALF_DARK", "games": n, "obs_format": args.fmt,
                    "mean_legal_actions": round(kbar, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(f"jq::k_observe<{ {'f32': 0, 'bf16': 1, 'u8': 2}[args.fmt] }>", n),
                      "kernel": f"k_observe<{args.fmt}>", "kernel_ms": round(obs_ms, 4),
                      "bytes_per_launch": obs_bytes},
         "wall_s": round(wall, 3),
