@@ -119,8 +119,10 @@ int jq_legal(jq_env *env, const int8_t *acting, int32_t *counts, int32_t *offset
 /* Observation of `observer` (device int8 N; NULL = current turn) in that seat's
  * canonical frame. fmt JQ_OBS_*; spatial: device (N,317,17,17) of the format's
  * element type; aux: device float (N,6,17,17) for JQ_OBS_U8 (else NULL);
- * global: device float (N,28). all_seats != 0 writes (N,4,...) for observers
- * 0..3 and ignores `observer`. Replaces build_observation_single_seat /
+ * global: device float (N,28). all_seats != 0 writes (N,4,...) rows; then
+ * `observer` is an optional device int8 (N,4) observer map (slot k of env i
+ * observes seat observer[i*4+k]; NULL = seat k), as upload_observer_seats sets
+ * it (junqi_rl/gpu_rollout.py:983-1001). Replaces build_observation_single_seat /
  * build_observation_batch_resident (observation.cu:648-802). */
 int jq_observe(jq_env *env, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial,
                float *aux, float *global, void *stream);
@@ -187,6 +189,9 @@ int jq_field_ptr(jq_env *env, int32_t field, void **dev_ptr);
  * four beliefs from the current board (GameState.__post_init__, state.py:346-483;
  * BeliefTensor.initial, info_model.py:218-265). */
 int jq_finalize_import(jq_env *env, void *stream);
+/* Recompute every env's Zobrist hash from its current fields (after editing
+ * scalar fields such as the termination flags); beliefs are left as they are. */
+int jq_rehash(jq_env *env, void *stream);
 
 /* Synchronise `stream`. */
 int jq_sync(void *stream);

@@ -9,6 +9,8 @@ built; there is no CPU implementation behind it.
 from . import _lib
 from ._lib import AUX_CHANNELS, JunqiError
 from .batch import JunqiBatch, decode_table, generate_lineups, generate_pool, recency_table, zobrist_stream
+from .gpu_rollout import GpuRollout
+from .gpu_world import GpuWorld
 
-__all__ = ["JunqiBatch", "JunqiError", "AUX_CHANNELS", "decode_table", "generate_lineups",
-           "generate_pool", "recency_table", "zobrist_stream", "_lib"]
+__all__ = ["JunqiBatch", "GpuRollout", "GpuWorld", "JunqiError", "AUX_CHANNELS", "decode_table",
+           "generate_lineups", "generate_pool", "recency_table", "zobrist_stream", "_lib"]

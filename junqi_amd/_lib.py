@@ -39,7 +39,8 @@ _EXPORTS = [
     "jq_upload_recency", "jq_upload_setup_pool", "jq_reset_lineups", "jq_reset_seeded",
     "jq_generate_lineups", "jq_generate_pool", "jq_board_tables", "jq_reset_terminated", "jq_step",
     "jq_legal", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_env_step",
-    "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import", "jq_sync",
+    "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import", "jq_rehash",
+    "jq_sync",
 ]
 
 
@@ -76,7 +77,8 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_field_info": ([I32, C.POINTER(I32), C.POINTER(I32)], C.c_int),
         "jq_get_field": ([P, I32, P], C.c_int), "jq_set_field": ([P, I32, P], C.c_int),
         "jq_field_ptr": ([P, I32, C.POINTER(P)], C.c_int),
-        "jq_finalize_import": ([P, P], C.c_int), "jq_sync": ([P], C.c_int),
+        "jq_finalize_import": ([P, P], C.c_int), "jq_rehash": ([P, P], C.c_int),
+        "jq_sync": ([P], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

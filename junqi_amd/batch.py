@@ -57,6 +57,11 @@ def decode_table() -> np.ndarray:
     return out
 
 
+_CM_FIELDS = ("cm_direct_lo", "cm_direct_hi", "cm_direct_type", "cm_last_direct", "cm_other_count",
+              "cm_chain_lo", "cm_chain_hi", "cm_chain_type", "cm_last_chain", "cm_eaten_lo", "cm_eaten_hi",
+              "cm_floor", "cm_floor_step", "cm_flags")
+
+
 class _CudaArrayView:
     """__cuda_array_interface__ wrapper so torch can view library-owned memory."""
 
@@ -257,6 +262,90 @@ class JunqiBatch:
 
     def finalize_import(self) -> None:
         check(lib.jq_finalize_import(self._h, self.stream))
+
+    def import_state(self, sd: dict, *, terminated=None, winner_team=None, draw=None,
+                     move_history=None) -> None:
+        """Load every env from the flat SoA dict that the reference's
+        ``DeviceGameStateBatch.copy_from_host`` takes (keys of
+        junqi_rl/gpu_rollout.py:448-483: per-piece arrays of N*120, cell_piece_id
+        of N*289, seat arrays of N*4, per-env turn / move_counter /
+        moves_since_last_combat). Combat memory starts empty and beliefs are
+        re-seeded from the board, as GameState.__post_init__ does for a state
+        built from arrays (state.py:346-483); the Zobrist hash is recomputed.
+        move_history: optional list (one per env) of (src_flat, dst_flat)
+        pairs, most recent last."""
+        n = self.n
+
+        def arr(key, shape, dt):
+            if key not in sd:
+                raise KeyError(f"import_state: missing key {key!r}")
+            a = np.asarray(sd[key])
+            if a.size != int(np.prod(shape)):
+                raise ValueError(f"import_state: {key} has {a.size} elements, expected {int(np.prod(shape))}")
+            return a.reshape(shape).astype(dt, copy=False)
+
+        alive = arr("alive", (n, 120), bool)
+        ptype = arr("piece_type_arr", (n, 120), np.int16)
+        px, py = arr("pos_x", (n, 120), np.int16), arr("pos_y", (n, 120), np.int16)
+        zx, zy = arr("zero_x", (n, 120), np.int16), arr("zero_y", (n, 120), np.int16)
+        cpid = arr("cell_piece_id", (n, 289), np.int16)
+
+        def pid128(a, fill, dt):
+            out = np.full((n, 128), fill, dt)
+            out[:, :120] = a
+            return out
+        cell = np.full((n, 292), -1, np.int8)
+        cell[:, :289] = cpid
+        self.set_field("cell", cell)
+        self.set_field("ptype", pid128(np.where(ptype > 0, ptype, -1), -1, np.int8))
+        self.set_field("pos", pid128(np.where(alive & (px >= 0) & (py >= 0), py * 17 + px, -1), -1, np.int16))
+        self.set_field("zero", pid128(np.where((zx >= 0) & (zy >= 0), zy * 17 + zx, -1), -1, np.int16))
+        for ours, key in (("move_count", "move_count_arr"), ("active_eat", "active_eat_arr"),
+                          ("passive_surv", "passive_surv_arr")):
+            self.set_field(ours, pid128(arr(key, (n, 120), np.int16), 0, np.int16))
+        self.set_field("death_reason", pid128(arr("death_reason_arr", (n, 120), np.int8), -1, np.int8))
+        self.set_field("death_step", pid128(arr("death_step_arr", (n, 120), np.int16), -1, np.int16))
+        self.set_field("death_loc", pid128(arr("death_loc_flat_arr", (n, 120), np.int16), -1, np.int16))
+        for name in _CM_FIELDS:
+            e, _ = L.field_info(name)
+            fill = -1 if name in ("cm_last_direct", "cm_last_chain", "cm_floor_step") else 0
+            self.set_field(name, np.full((n, e), fill, np.int64))
+        bits = np.arange(4, dtype=np.uint8)
+        self.set_field("seat_dead", (arr("seat_dead_arr", (n, 4), np.uint8) << bits).sum(-1).astype(np.uint8))
+        self.set_field("flag_rev", (arr("seat_flag_revealed_arr", (n, 4), np.uint8) << bits).sum(-1).astype(np.uint8))
+        self.set_field("turn", arr("turn", (n,), np.int8))
+        self.set_field("move_counter", arr("move_counter", (n,), np.int32))
+        self.set_field("mslc", arr("moves_since_last_combat", (n,), np.int32))
+        hist = np.zeros((n, 32), np.int32)
+        meta = np.zeros((n, 1), np.int32)
+        for i, h in enumerate(move_history or []):
+            h = list(h)[-32:]
+            for k, (s, d) in enumerate(h):
+                hist[i, k] = int(s) | (int(d) << 16)
+            meta[i, 0] = len(h) | ((len(h) & 31) << 8)
+        self.set_field("hist", hist)
+        self.set_field("hist_meta", meta)
+        self.set_termination(np.zeros(n, bool) if terminated is None else terminated,
+                             np.full(n, -1, np.int8) if winner_team is None else winner_team,
+                             np.zeros(n, bool) if draw is None else draw, finalize=False)
+        self.finalize_import()
+
+    def set_termination(self, terminated, winner_team, draw, *, finalize: bool = True) -> None:
+        """Overwrite the per-env terminated / winner_team / draw flags
+        (copy_termination_from_host, bindings.cpp:200-243); the Zobrist hash is
+        recomputed when `finalize`."""
+        n = self.n
+        self.set_field("terminated", np.asarray(terminated).reshape(n).astype(np.uint8))
+        self.set_field("winner", np.asarray(winner_team).reshape(n).astype(np.int8))
+        self.set_field("draw", np.asarray(draw).reshape(n).astype(np.uint8))
+        if finalize:
+            check(lib.jq_rehash(self._h, self.stream))
+
+    def termination(self) -> dict[str, np.ndarray]:
+        """terminated / winner_team / draw on the host (copy_termination_to_host)."""
+        return {"terminated": self.get_field("terminated")[:, 0].astype(bool),
+                "winner_team": self.get_field("winner")[:, 0].astype(np.int8),
+                "draw": self.get_field("draw")[:, 0].astype(bool)}
 
     def field_tensor(self, name: str, torch_dtype: torch.dtype | None = None) -> torch.Tensor:
         """Zero-copy device view of a per-env state field, shape (N, elems) or (N,)."""

@@ -675,8 +675,9 @@ __global__ __launch_bounds__(64) void k_reset_terminated(State S, int64_t seed)
     init_env(S, env, S.pool + (size_t)idx * NP);
 }
 
-// Recompute Zobrist and re-seed beliefs from the current board (hand-built states).
-__global__ __launch_bounds__(64) void k_finalize(State S)
+// Recompute Zobrist and (if `beliefs`) re-seed beliefs from the current board
+// (hand-built states).
+__global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
 {
     const int env = blockIdx.x, l = threadIdx.x;
     if (env >= S.n) return;
@@ -685,7 +686,7 @@ __global__ __launch_bounds__(64) void k_finalize(State S)
         const size_t pi = (size_t)env * PID_STRIDE + p;
         const int f = S.pos[pi], t = S.ptype[pi];
         if (f >= 0 && t >= 0) z ^= zp(S.ztab, p, t, f);
-        for (int o = 0; o < 4; ++o) {
+        for (int o = 0; o < 4 && beliefs; ++o) {
             uint8_t code = 0;
             if (f >= 0 && t >= 2) {
                 if (sees_truth(o, p / 30, S.show_mode)) code = (uint8_t)(1 + t - 2);
@@ -696,14 +697,14 @@ __global__ __launch_bounds__(64) void k_finalize(State S)
     }
     z = wave_xor(z);
     static constexpr int8_t kCounts[12] = {1, 3, 2, 1, 1, 2, 2, 2, 2, 3, 3, 3};
-    if (l < 48) {
+    if (beliefs && l < 48) {
         for (int o = 0; o < 4; ++o) {
             const int s = l / 12, t = l % 12;
             const bool tracked_seat = s != o && ((s & 1) != (o & 1));
             S.rem[((size_t)env * 4 + o) * 48 + l] = tracked_seat ? kCounts[t] : 0;
         }
     }
-    if (l < 4) {
+    if (beliefs && l < 4) {
         uint8_t trk = 0;
         for (int s = 0; s < 4; ++s) if (s != l && ((s & 1) != (l & 1))) trk |= (uint8_t)(1u << s);
         S.remtrk[(size_t)env * 4 + l] = trk;

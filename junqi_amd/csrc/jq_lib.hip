@@ -511,10 +511,19 @@ int jq_finalize_import(jq_env *e, void *stream)
     int rc = check_env(e);
     if (rc) return rc;
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables first");
-    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S);
+    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 1);
     if ((rc = launch_check("k_finalize")) != 0) return rc;
     HIP_TRY(hipStreamSynchronize(strm(stream)));
     return JQ_OK;
+}
+
+int jq_rehash(jq_env *e, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables first");
+    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 0);
+    return launch_check("k_finalize");
 }
 
 int jq_sync(void *stream)

@@ -293,11 +293,13 @@ struct RowIn {
 
 __device__ __forceinline__ int row_env(int row, int all_seats) { return all_seats ? row >> 2 : row; }
 
+// Observer of a row: all_seats rows take observer[env * 4 + k] (k-th slot of the
+// env's (N,4) observer map, default seat k); single rows take observer[env] or
+// the env's acting seat.
 __device__ __forceinline__ int row_obs(const State &S, const int8_t *observer, int all_seats, int row)
 {
-    if (all_seats) return row & 3;
-    const int env = row;
-    return (observer ? observer[env] : S.turn[env]) & 3;
+    if (all_seats) return (observer ? observer[row] : row) & 3;
+    return (observer ? observer[row] : S.turn[row]) & 3;
 }
 
 // Seat of the observer's i-th relation in plane order: self, teammate, left, right.

@@ -126,3 +126,29 @@ def test_packaged_recency_table_is_the_fixture():
 def test_zobrist_stream_matches_oracle(jl):
     from junqi_amd.batch import zobrist_stream
     assert np.array_equal(zobrist_stream(), O.zobrist_tables())
+
+
+def test_mirror_helpers_without_gpu():
+    """Argument handling of the GpuRollout / GpuWorld mirrors that needs no device."""
+    import types
+
+    from junqi_amd.gpu_rollout import _show_value
+    from junqi_amd.gpu_world import _pack_state_arrays
+
+    assert _show_value(1) == 1 and _show_value(types.SimpleNamespace(value=2)) == 2
+    with pytest.raises(ValueError):
+        _show_value(3)
+    g = O.Game(O.random_setup(5))
+    b = g.buf[0]
+    st = types.SimpleNamespace(
+        alive=b["alive"].astype(bool), piece_type_arr=b["ptype"], piece_seat_arr=b["pseat"], pos_x=b["pos_x"],
+        pos_y=b["pos_y"], zero_x=b["zero_x"], zero_y=b["zero_y"], move_count_arr=b["move_count"],
+        active_eat_arr=b["active_eat"], passive_surv_arr=b["passive_surv"], death_reason_arr=b["death_reason"],
+        death_step_arr=b["death_step"], death_loc_flat_arr=b["death_loc"], cell_piece_id=b["cell_pid"],
+        seat_dead_arr=b["seat_dead"].astype(bool), seat_flag_revealed_arr=b["flag_rev"].astype(bool),
+        turn=types.SimpleNamespace(value=2), move_counter=7, moves_since_last_combat=3, terminated=False,
+        winner_team=None, draw=False, move_history=[(10, 27)])
+    sd, extra = _pack_state_arrays([types.SimpleNamespace(state=st)] * 2)
+    assert sd["alive"].shape == (240,) and sd["cell_piece_id"].shape == (578,) and sd["seat_dead_arr"].shape == (8,)
+    assert sd["turn"].tolist() == [2, 2] and sd["move_counter"].tolist() == [7, 7]
+    assert extra["winner_team"].tolist() == [-1, -1] and extra["move_history"] == [[(10, 27)], [(10, 27)]]
