@@ -183,8 +183,11 @@ enum jq_field {
 int jq_field_info(int32_t field, int32_t *elems_per_env, int32_t *elem_bytes);
 int jq_get_field(jq_env *env, int32_t field, void *host_dst);
 int jq_set_field(jq_env *env, int32_t field, const void *host_src);
-/* Device address of a state field (zero-copy views, e.g. turn_torch). */
-int jq_field_ptr(jq_env *env, int32_t field, void **dev_ptr);
+/* Device address of element 0 of a state field and its strides in bytes between
+ * envs and between a field's elements (zero-copy strided views, e.g. turn_torch:
+ * junqi_rl/gpu_rollout.py:1159-1193). Fields live inside per-piece, per-observer
+ * and per-env records, so the strides are generally larger than the element. */
+int jq_field_ptr(jq_env *env, int32_t field, void **dev_ptr, int64_t *env_stride, int64_t *elem_stride);
 /* After jq_set_field edits: recompute every env's Zobrist hash and re-seed the
  * four beliefs from the current board (GameState.__post_init__, state.py:346-483;
  * BeliefTensor.initial, info_model.py:218-265). */

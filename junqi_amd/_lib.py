@@ -76,7 +76,7 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_env_step": ([P, P, U64, U64, I64, P, P, P, P, I32, P, P, P, P, P, P, P], C.c_int),
         "jq_field_info": ([I32, C.POINTER(I32), C.POINTER(I32)], C.c_int),
         "jq_get_field": ([P, I32, P], C.c_int), "jq_set_field": ([P, I32, P], C.c_int),
-        "jq_field_ptr": ([P, I32, C.POINTER(P)], C.c_int),
+        "jq_field_ptr": ([P, I32, C.POINTER(P), C.POINTER(I64), C.POINTER(I64)], C.c_int),
         "jq_finalize_import": ([P, P], C.c_int), "jq_rehash": ([P, P], C.c_int),
         "jq_sync": ([P], C.c_int),
     }

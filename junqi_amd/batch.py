@@ -65,9 +65,9 @@ _CM_FIELDS = ("cm_direct_lo", "cm_direct_hi", "cm_direct_type", "cm_last_direct"
 class _CudaArrayView:
     """__cuda_array_interface__ wrapper so torch can view library-owned memory."""
 
-    def __init__(self, ptr: int, shape: tuple[int, ...], typestr: str):
+    def __init__(self, ptr: int, shape: tuple[int, ...], typestr: str, strides: tuple[int, ...] | None = None):
         self.__cuda_array_interface__ = {"data": (int(ptr), False), "shape": tuple(shape),
-                                         "typestr": typestr, "version": 2}
+                                         "typestr": typestr, "strides": strides, "version": 2}
 
 
 _TYPESTR = {(1, "i"): "|i1", (1, "u"): "|u1", (2, "i"): "<i2", (2, "u"): "<u2", (4, "i"): "<i4",
@@ -348,16 +348,16 @@ class JunqiBatch:
                 "draw": self.get_field("draw")[:, 0].astype(bool)}
 
     def field_tensor(self, name: str, torch_dtype: torch.dtype | None = None) -> torch.Tensor:
-        """Zero-copy device view of a per-env state field, shape (N, elems) or (N,)."""
+        """Zero-copy (strided) device view of a per-env state field, shape (N, elems) or (N,)."""
         e, b = L.field_info(name)
-        ptr = C.c_void_p()
-        check(lib.jq_field_ptr(self._h, L.FIELDS[name], C.byref(ptr)))
+        ptr, es, ls = C.c_void_p(), C.c_int64(), C.c_int64()
+        check(lib.jq_field_ptr(self._h, L.FIELDS[name], C.byref(ptr), C.byref(es), C.byref(ls)))
         kind = _FIELD_KIND.get(name, "i")
         ts = _TYPESTR[(b, kind)]
         if torch_dtype is torch.bool:
             ts = "|b1"
-        shape = (self.n,) if e == 1 else (self.n, e)
-        return torch.as_tensor(_CudaArrayView(ptr.value, shape, ts), device=self.device)
+        shape, strides = ((self.n,), (es.value,)) if e == 1 else ((self.n, e), (es.value, ls.value))
+        return torch.as_tensor(_CudaArrayView(ptr.value, shape, ts, strides), device=self.device)
 
     def sync(self) -> None:
         torch.cuda.synchronize(self.device)

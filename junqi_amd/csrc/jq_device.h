@@ -26,42 +26,70 @@ enum : uint8_t { CMF_IS_GONGB = 1, CMF_NOT_GONGB = 2, CMF_ATK_GONGB = 4 };
 // belief row codes: 0 zero, 1..12 one-hot(tracked idx+1), 16+slot prior row, 64 uniform
 constexpr int BC_PRIOR0 = 16, BC_UNIFORM = 64, BC_COUNT = 65;
 
-// Struct of device pointers; one handle owns all of them. Per-env blocks are
-// contiguous so the wave that owns an env reads its rows with coalesced loads.
+// One piece id of one env: everything the rules keep per piece, in one 16-byte
+// record so a lane fetches it with a single dwordx4 load.
+struct alignas(16) PieceRec {
+    int16_t pos, zero;       // flat cells (-1 dead / none)
+    int16_t dstep, dloc;     // death step and cell (-1 alive)
+    int16_t mcount, aeat, psurv;
+    int8_t ptype, dreason;   // PieceType (-1 absent), DeathReason (-1 alive)
+};
+static_assert(sizeof(PieceRec) == 16, "piece record must be 16 bytes");
+
+// CombatMemory v6 of one (observer, pid) (combat_memory.py:251-311).
+struct alignas(16) CmRec {
+    uint64_t dlo, dhi;       // pids killed directly (120-bit set)
+    uint64_t clo, chi;       // pids killed directly or by chain
+    uint64_t elo, ehi;       // pids this (own) piece was eaten by
+    uint16_t dtype, ctype;   // tracked types killed directly / by chain (12 bits)
+    int16_t ldir, ocnt, lchain, fstep;  // last direct step, other count, last chain step, floor step
+    int8_t floor;
+    uint8_t flags;           // CMF_*
+    uint16_t pad;
+};
+static_assert(sizeof(CmRec) == 64, "combat-memory record must be 64 bytes");
+
+// Per-env scalars.
+struct alignas(16) EnvRec {
+    uint64_t zob;
+    int32_t mc, mslc;        // move counter, moves since last combat
+    int32_t hmeta;           // move-history count | head << 8
+    int8_t turn;
+    uint8_t term;
+    int8_t winner;           // -1 / 0 / 1
+    uint8_t draw, sdead, sflag;   // seat bitmasks
+    uint8_t remtrk[4];       // per observer: bit s = remaining[s] tracked
+    uint8_t pad[2];
+};
+static_assert(sizeof(EnvRec) == 32, "env record must be 32 bytes");
+
+// Legal-set scratch between k_legal and k_emit: per movable piece (ascending
+// source cell) its 129-bit compact destination mask.
+struct alignas(16) LegalRec {
+    uint64_t mask[32][3];
+    int16_t src[32];
+    int32_t n, seat;
+    int32_t pad[2];
+};
+
+// One handle's device arrays. Per-env blocks are contiguous so the wave that
+// owns an env reads its rows with coalesced loads.
 struct State {
     int32_t n, max_moves, show_mode, pool_size;
     int8_t *cell;          // [n][292]
-    int8_t *ptype;         // [n][128]
-    int16_t *pos, *zero;   // [n][128]
-    int16_t *mcount, *aeat, *psurv;
-    int8_t *dreason;
-    int16_t *dstep, *dloc;
+    PieceRec *piece;       // [n][128]
+    CmRec *cm;             // [n][4][128]
     uint8_t *bcode;        // [n][4][128]
     int8_t *rem;           // [n][4][4][12]
-    uint8_t *remtrk;       // [n][4]
-    uint64_t *cm_dlo, *cm_dhi, *cm_clo, *cm_chi, *cm_elo, *cm_ehi;  // [n][4][128]
-    uint16_t *cm_dtype, *cm_ctype;
-    int16_t *cm_ldir, *cm_ocnt, *cm_lchain, *cm_fstep;
-    int8_t *cm_floor;
-    uint8_t *cm_flags;
+    EnvRec *env;           // [n]
     int32_t *hist;         // [n][32]
-    int32_t *hmeta;        // [n]  count | head << 8
-    int8_t *turn;
-    uint8_t *term;
-    int8_t *winner;
-    uint8_t *draw, *sdead, *sflag;
-    int32_t *mc, *mslc;
-    uint64_t *zob;
+    LegalRec *lg;          // [n]
     const uint64_t *ztab;  // Zobrist stream
     const float *rlut;     // [4][4096]
     const int8_t *pool;    // [pool_size][120]
-    // legal-set scratch consumed by the CSR emit kernel
-    int16_t *lg_src;       // [n][32]
-    uint64_t *lg_mask;     // [n][32][3]
-    int32_t *lg_n;         // [n]
-    int8_t *lg_seat;       // [n]
 };
 
 __device__ __forceinline__ size_t cm_idx(int env, int o, int pid) { return ((size_t)env * 4 + o) * PID_STRIDE + pid; }
+__device__ __forceinline__ size_t pc_idx(int env, int pid) { return (size_t)env * PID_STRIDE + pid; }
 
 }  // namespace jq

@@ -148,7 +148,7 @@ __device__ void piece_mask_lane(const int8_t *cell, int src, int team, bool engi
 
 // dst on a straight run (k < 4) or curve run of src with every earlier cell empty
 // (move_gen.py:127-171 and 384-423).
-__device__ bool run_clear(const int8_t *cell, int src, int dst, bool curve)
+__device__ __forceinline__ bool run_clear(const int8_t *cell, int src, int dst, bool curve)
 {
     const int r = cT.railidx[src];
     if (r < 0) return false;
@@ -164,7 +164,7 @@ __device__ bool run_clear(const int8_t *cell, int src, int dst, bool curve)
     return false;
 }
 
-__device__ bool engineer_reaches(const int8_t *cell, int src, int dst)
+__device__ __forceinline__ bool engineer_reaches(const int8_t *cell, int src, int dst)
 {   // move_gen.py:186-224
     if (!is_rail(src) || !is_rail(dst) || src == dst) return false;
     uint64_t r0, r1;
@@ -174,7 +174,7 @@ __device__ bool engineer_reaches(const int8_t *cell, int src, int dst)
 }
 
 // is_legal_move (move_gen.py:299-376), uniform over the wave.
-__device__ bool legal_pair(const int8_t *cell, const int8_t *ptype, int seat, int src, int dst)
+__device__ __forceinline__ bool legal_pair(const int8_t *cell, const int8_t *ptype, int seat, int src, int dst)
 {
     if (src < 0 || src >= NC || dst < 0 || dst >= NC || src == dst) return false;
     if (!is_on(src) || !is_on(dst)) return false;
@@ -198,7 +198,7 @@ __device__ bool legal_pair(const int8_t *cell, const int8_t *ptype, int seat, in
 }
 
 // move_requires_gongb (move_gen.py:245-296) for a legal engineer move.
-__device__ bool engineer_only(const int8_t *cell, int src, int dst)
+__device__ __forceinline__ bool engineer_only(const int8_t *cell, int src, int dst)
 {
     const int sx = src % 17, sy = src / 17, dx = dst % 17, dy = dst / 17;
     const int adx = abs(sx - dx), ady = abs(sy - dy);
@@ -214,7 +214,7 @@ __device__ bool engineer_only(const int8_t *cell, int src, int dst)
 }
 
 // Does `seat` have a legal move (the Q12 test, state.py:1139-1165)?
-__device__ bool seat_has_move(const int8_t *cell, const int16_t *pos, const int8_t *ptype, int seat)
+__device__ __forceinline__ bool seat_has_move(const int8_t *cell, const int16_t *pos, const int8_t *ptype, int seat)
 {
     const int l = lane_id(), team = seat & 1;
     bool mov = false, quick = false, eng = false;
@@ -292,8 +292,8 @@ __device__ void kill_piece(const State &S, int env, int8_t *cell, int16_t *pos, 
     __syncthreads();
     if (lane_id() == 0) {
         cell[cur] = -1; pos[pid] = -1;
-        const size_t pi = (size_t)env * PID_STRIDE + pid;
-        S.pos[pi] = -1; S.dreason[pi] = (int8_t)reason; S.dstep[pi] = (int16_t)step; S.dloc[pi] = (int16_t)loc;
+        PieceRec &r = S.piece[pc_idx(env, pid)];
+        r.pos = -1; r.dreason = (int8_t)reason; r.dstep = (int16_t)step; r.dloc = (int16_t)loc;
         S.cell[(size_t)env * CELL_STRIDE + cur] = -1;
     }
     __syncthreads();
@@ -309,7 +309,7 @@ __device__ void move_piece(const State &S, int env, int8_t *cell, int16_t *pos, 
         cell[src] = -1; cell[dst] = (int8_t)pid; pos[pid] = (int16_t)dst;
         S.cell[(size_t)env * CELL_STRIDE + src] = -1;
         S.cell[(size_t)env * CELL_STRIDE + dst] = (int8_t)pid;
-        S.pos[(size_t)env * PID_STRIDE + pid] = (int16_t)dst;
+        S.piece[pc_idx(env, pid)].pos = (int16_t)dst;
     }
     __syncthreads();
 }
@@ -328,8 +328,8 @@ __device__ void purge_seat(const State &S, int env, int8_t *cell, int16_t *pos, 
         if ((unsigned)cur < (unsigned)NC) {
             z = zp(S.ztab, pid, ptype[pid], cur);
             cell[cur] = -1; pos[pid] = -1;
-            const size_t pi = (size_t)env * PID_STRIDE + pid;
-            S.pos[pi] = -1; S.dreason[pi] = 0; S.dstep[pi] = (int16_t)step; S.dloc[pi] = (int16_t)cur;
+            PieceRec &r = S.piece[pc_idx(env, pid)];
+            r.pos = -1; r.dreason = 0; r.dstep = (int16_t)step; r.dloc = (int16_t)cur;
             S.cell[(size_t)env * CELL_STRIDE + cur] = -1;
         }
     }
@@ -338,8 +338,9 @@ __device__ void purge_seat(const State &S, int env, int8_t *cell, int16_t *pos, 
 }
 
 // CombatMemory update for EAT / KILLED (combat_memory.py:354-569). Lane o < 4
-// handles observer o; observers never touch each other's rows.
-__device__ void cm_apply(const State &S, int env, bool is_eat, int apid, int dpid, int aseat, int dseat,
+// handles observer o; observers never touch each other's records. K is the
+// surviving piece, V the killed one; V's own kills cannot include K (K is alive).
+__device__ __forceinline__ void cm_apply(const State &S, int env, bool is_eat, int apid, int dpid, int aseat, int dseat,
                          int atype, int dtype, int step)
 {
     const int o = lane_id();
@@ -348,23 +349,20 @@ __device__ void cm_apply(const State &S, int env, bool is_eat, int apid, int dpi
     if (is_eat) { K = apid; V = dpid; Vs = dseat; Vt = dtype; }
     else        { K = dpid; V = apid; Vs = aseat; Vt = atype; }
     const size_t kI = cm_idx(env, o, K), vI = cm_idx(env, o, V);
-    uint8_t kflags = S.cm_flags[kI];
-    const uint8_t vflags = S.cm_flags[vI];
+    CmRec k = S.cm[kI];
+    const CmRec v = S.cm[vI];
     if (!is_eat) {
-        const bool known = (vflags & CMF_IS_GONGB) || (atype == T_GONGB && o == Vs);
-        if (known) kflags |= CMF_ATK_GONGB;
+        const bool known = (v.flags & CMF_IS_GONGB) || (atype == T_GONGB && o == Vs);
+        if (known) k.flags |= CMF_ATK_GONGB;
     }
-    const uint64_t vdlo = S.cm_dlo[vI], vdhi = S.cm_dhi[vI], vclo = S.cm_clo[vI], vchi = S.cm_chi[vI];
-    uint64_t kclo = S.cm_clo[kI] | vdlo | vclo, kchi = S.cm_chi[kI] | vdhi | vchi;
-    if (V < 64) kclo |= 1ull << V; else kchi |= 1ull << (V - 64);
-    uint16_t kctype = (uint16_t)(S.cm_ctype[kI] | S.cm_dtype[vI] | S.cm_ctype[vI]);
-    int kfloor = S.cm_floor[kI];
-    int16_t kfstep = S.cm_fstep[kI];
-    const int vfloor = S.cm_floor[vI];
-    if (vfloor > 0) {
-        const int prop = vfloor + 1 < 9 ? vfloor + 1 : 9;
-        if (prop > kfloor) { kfloor = prop; kfstep = (int16_t)step; }
-        kflags |= CMF_NOT_GONGB;
+    k.clo |= v.dlo | v.clo;
+    k.chi |= v.dhi | v.chi;
+    if (V < 64) k.clo |= 1ull << V; else k.chi |= 1ull << (V - 64);
+    k.ctype = (uint16_t)(k.ctype | v.dtype | v.ctype);
+    if (v.floor > 0) {
+        const int prop = v.floor + 1 < 9 ? v.floor + 1 : 9;
+        if (prop > k.floor) { k.floor = (int8_t)prop; k.fstep = (int16_t)step; }
+        k.flags |= CMF_NOT_GONGB;
     }
     // v6 reverse projection: observer's own pids V had eaten (directly or by chain),
     // plus V itself when V belongs to the observer, are now eaten by K too.
@@ -372,48 +370,43 @@ __device__ void cm_apply(const State &S, int env, bool is_eat, int apid, int dpi
         uint64_t mlo = 0, mhi = 0;
         const int b0 = o * 30;
         for (int s = 0; s < 30; ++s) { const int gp = b0 + s; if (gp < 64) mlo |= 1ull << gp; else mhi |= 1ull << (gp - 64); }
-        uint64_t vlo = (vdlo | vclo) & mlo, vhi = (vdhi | vchi) & mhi;
+        uint64_t vlo = (v.dlo | v.clo) & mlo, vhi = (v.dhi | v.chi) & mhi;
         if (Vs == o) { if (V < 64) vlo |= 1ull << V; else vhi |= 1ull << (V - 64); }
         const uint64_t klo = K < 64 ? (1ull << K) : 0ull, khi = K >= 64 ? (1ull << (K - 64)) : 0ull;
-        while (vlo) { const int b = __builtin_ctzll(vlo); vlo &= vlo - 1; const size_t t = cm_idx(env, o, b); S.cm_elo[t] |= klo; S.cm_ehi[t] |= khi; }
-        while (vhi) { const int b = __builtin_ctzll(vhi) + 64; vhi &= vhi - 1; const size_t t = cm_idx(env, o, b); S.cm_elo[t] |= klo; S.cm_ehi[t] |= khi; }
+        while (vlo) { const int b = __builtin_ctzll(vlo); vlo &= vlo - 1; CmRec &t = S.cm[cm_idx(env, o, b)]; t.elo |= klo; t.ehi |= khi; }
+        while (vhi) { const int b = __builtin_ctzll(vhi) + 64; vhi &= vhi - 1; CmRec &t = S.cm[cm_idx(env, o, b)]; t.elo |= klo; t.ehi |= khi; }
     }
-    int16_t kldir = S.cm_ldir[kI];
     if (Vs != o) {
-        const int c = S.cm_ocnt[kI] + 1;
-        S.cm_ocnt[kI] = (int16_t)(c < 32767 ? c : 32767);
-        kldir = (int16_t)step;
+        const int c = k.ocnt + 1;
+        k.ocnt = (int16_t)(c < 32767 ? c : 32767);
     } else {
-        uint64_t kdlo = S.cm_dlo[kI], kdhi = S.cm_dhi[kI];
-        if (V < 64) kdlo |= 1ull << V; else kdhi |= 1ull << (V - 64);
-        S.cm_dlo[kI] = kdlo; S.cm_dhi[kI] = kdhi;
+        if (V < 64) k.dlo |= 1ull << V; else k.dhi |= 1ull << (V - 64);
         const int vi = tracked(Vt);
         if (vi >= 0) {
-            S.cm_dtype[kI] = (uint16_t)(S.cm_dtype[kI] | (1u << vi));
-            kctype |= (uint16_t)(1u << vi);
+            k.dtype = (uint16_t)(k.dtype | (1u << vi));
+            k.ctype = (uint16_t)(k.ctype | (1u << vi));
         }
-        kldir = (int16_t)step;
-        if (is_eat) kflags |= (Vt == T_DILEI) ? CMF_IS_GONGB : CMF_NOT_GONGB;
+        if (is_eat) k.flags |= (Vt == T_DILEI) ? CMF_IS_GONGB : CMF_NOT_GONGB;
         if (Vt >= T_SILING && Vt <= T_GONGB) {
             const int pr = rank_floor_next(Vt);
-            if (pr > kfloor) { kfloor = pr; kfstep = (int16_t)step; }
+            if (pr > k.floor) { k.floor = (int8_t)pr; k.fstep = (int16_t)step; }
         }
     }
-    S.cm_clo[kI] = kclo; S.cm_chi[kI] = kchi; S.cm_ctype[kI] = kctype;
-    S.cm_lchain[kI] = (int16_t)step; S.cm_ldir[kI] = kldir;
-    S.cm_floor[kI] = (int8_t)kfloor; S.cm_fstep[kI] = kfstep; S.cm_flags[kI] = kflags;
+    k.ldir = (int16_t)step;
+    k.lchain = (int16_t)step;
+    S.cm[kI] = k;
 }
 
 // BeliefTensor.update for the four observers (info_model.py:271-429). Entries are
 // keyed by pid so R1 migration is implicit; lane o < 4 handles observer o.
-__device__ void belief_update(const State &S, int env, const int8_t *cell, int sp, int dp, int ss, int ds,
+__device__ __forceinline__ void belief_update(const State &S, int env, const int8_t *cell, int sp, int dp, int ss, int ds,
                               int dt, int dst, int ev, bool rsrc, bool rdst, bool fcap, int died)
 {
     const int o = lane_id();
     if (o >= 4) return;
     uint8_t *bc = S.bcode + ((size_t)env * 4 + o) * PID_STRIDE;
     int8_t *rem = S.rem + ((size_t)env * 4 + o) * 48;
-    uint8_t trk = S.remtrk[(size_t)env * 4 + o];
+    uint8_t trk = S.env[env].remtrk[o];
     auto dec = [&](int seat, int ti) {
         if ((trk >> seat) & 1) { int8_t &c = rem[seat * 12 + ti]; if (c > 0) --c; }
     };
@@ -438,7 +431,7 @@ __device__ void belief_update(const State &S, int env, const int8_t *cell, int s
     else if (ev == EV_KILLED) removed(ss, acode);
     else if (ev == EV_BOMB) { removed(ss, acode); if (dp >= 0) removed(ds, dcode); }
     trk &= (uint8_t)~died;
-    S.remtrk[(size_t)env * 4 + o] = trk;
+    S.env[env].remtrk[o] = trk;
 }
 
 __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict__ actions,
@@ -450,14 +443,15 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     __shared__ int16_t pos[PID_STRIDE];
     __shared__ int8_t ptype[PID_STRIDE];
 
-    const bool was_term = S.term[env] != 0;
-    const int seat = S.turn[env];
+    const EnvRec &E = S.env[env];   // uniform: scalar loads
+    const bool was_term = E.term != 0;
+    const int seat = E.turn;
     if (l == 0) {
         if (O.valid) O.valid[env] = 0;
         if (O.event) O.event[env] = 0;
         if (O.term) O.term[env] = was_term;
-        if (O.winner) O.winner[env] = S.winner[env];
-        if (O.draw) O.draw[env] = S.draw[env];
+        if (O.winner) O.winner[env] = E.winner;
+        if (O.draw) O.draw[env] = E.draw;
         if (O.fcap) O.fcap[env] = 0;
         if (O.died) O.died[env] = 0;
         if (O.reward) O.reward[env] = 0.f;
@@ -479,45 +473,42 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     if (l == 0 && O.world && src >= 0) O.world[env] = src * NC + dst;
     if (src < 0) return;
     if (acting && acting[env] != seat) return;
-    const uint8_t sdead0 = S.sdead[env];
+    const uint8_t sdead0 = E.sdead;
     if ((sdead0 >> seat) & 1) return;
 
     for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
     for (int p = l; p < PID_STRIDE; p += 64) {
-        pos[p] = S.pos[(size_t)env * PID_STRIDE + p];
-        ptype[p] = S.ptype[(size_t)env * PID_STRIDE + p];
+        const PieceRec r = S.piece[pc_idx(env, p)];
+        pos[p] = r.pos;
+        ptype[p] = r.ptype;
     }
     __syncthreads();
     if (!legal_pair(cell, ptype, seat, src, dst)) return;
 
-    const int mc0 = S.mc[env], mslc0 = S.mslc[env];
-    uint64_t zob = S.zob[env];
+    const int mc0 = E.mc, mslc0 = E.mslc;
+    uint64_t zob = E.zob;
     const uint64_t *Z = S.ztab;
     zob ^= Z[ZOFF_TURN + seat] ^ Z[ZOFF_MC + (mc0 & 0xFFF)] ^ Z[ZOFF_MSLC + (mslc0 & 0x1FF)];
     const int step = mc0 + 1;
     int died = 0;
-    uint8_t sdead = sdead0, sflag = S.sflag[env];
+    uint8_t sdead = sdead0, sflag = E.sflag;
     const int sp = cell[src], dp = cell[dst];
     const int st = ptype[sp], dt = dp >= 0 ? ptype[dp] : -1;
     const int ss = sp / 30, ds = dp >= 0 ? dp / 30 : -1;
 
     if (st == T_GONGB && engineer_only(cell, src, dst)) {
-        if (l < 4) S.cm_flags[cm_idx(env, l, sp)] |= CMF_IS_GONGB;
+        if (l < 4) S.cm[cm_idx(env, l, sp)].flags |= CMF_IS_GONGB;
     }
     // move history (state.py:673-678)
-    if (l == 0) {
-        const int meta = S.hmeta[env];
-        const int cnt = meta & 0xFF, head = (meta >> 8) & 31;
-        S.hist[(size_t)env * HIST_LEN + head] = src | (dst << 16);
-        S.hmeta[env] = (cnt < 32 ? cnt + 1 : 32) | (((head + 1) & 31) << 8);
-    }
+    const int hcnt = E.hmeta & 0xFF, hhead = (E.hmeta >> 8) & 31;
+    if (l == 0) S.hist[(size_t)env * HIST_LEN + hhead] = src | (dst << 16);
     int ev;
     bool rsrc = false, rdst = false, fcap = false;
     auto set_flag = [&](int s) { if (!((sflag >> s) & 1)) { sflag |= (uint8_t)(1u << s); zob ^= Z[ZOFF_SFLAG + s]; } };
     auto set_dead = [&](int s) { if (!((sdead >> s) & 1)) { sdead |= (uint8_t)(1u << s); zob ^= Z[ZOFF_SDEAD + s]; } };
     if (dp < 0) {
         ev = EV_MOVE;
-        if (l == 0) S.mcount[(size_t)env * PID_STRIDE + sp] += 1;
+        if (l == 0) S.piece[pc_idx(env, sp)].mcount += 1;
         move_piece(S, env, cell, pos, ptype, sp, src, dst, zob);
     } else {
         ev = resolve_combat(st, dt);
@@ -527,12 +518,12 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
         if (rsrc) set_flag(ss);
         if (rdst) set_flag(ds);
         if (ev == EV_EAT) {
-            if (l == 0) S.aeat[(size_t)env * PID_STRIDE + sp] += 1;
+            if (l == 0) S.piece[pc_idx(env, sp)].aeat += 1;
             kill_piece(S, env, cell, pos, ptype, dp, 0, dst, step, zob);
             move_piece(S, env, cell, pos, ptype, sp, src, dst, zob);
             cm_apply(S, env, true, sp, dp, ss, ds, st, dt, step);
         } else if (ev == EV_KILLED) {
-            if (l == 0) S.psurv[(size_t)env * PID_STRIDE + dp] += 1;
+            if (l == 0) S.piece[pc_idx(env, dp)].psurv += 1;
             kill_piece(S, env, cell, pos, ptype, sp, (dt == T_DILEI || dt == T_ZHADAN) ? 1 : 0, dst, step, zob);
             cm_apply(S, env, false, sp, dp, ss, ds, st, dt, step);
         } else {
@@ -589,9 +580,11 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     belief_update(S, env, cell, sp, dp, ss, ds, dt, dst, ev, rsrc, rdst, fcap, died);
 
     if (l == 0) {
-        S.mc[env] = nmc; S.mslc[env] = nmslc; S.turn[env] = (int8_t)nturn;
-        S.term[env] = (uint8_t)term; S.winner[env] = (int8_t)win; S.draw[env] = (uint8_t)drw;
-        S.sdead[env] = sdead; S.sflag[env] = sflag; S.zob[env] = zob;
+        EnvRec &W = S.env[env];   // remtrk belongs to belief_update's lanes
+        W.zob = zob; W.mc = nmc; W.mslc = nmslc;
+        W.hmeta = (hcnt < 32 ? hcnt + 1 : 32) | (((hhead + 1) & 31) << 8);
+        W.turn = (int8_t)nturn; W.term = (uint8_t)term; W.winner = (int8_t)win; W.draw = (uint8_t)drw;
+        W.sdead = sdead; W.sflag = sflag;
         if (O.valid) O.valid[env] = 1;
         if (O.event) O.event[env] = (int8_t)ev;
         if (O.term) O.term[env] = (uint8_t)term;
@@ -604,6 +597,32 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
 }
 
 // ------------------------------------------------------------------ reset
+// Empty, terminated state for every env (before the first reset).
+__global__ __launch_bounds__(64) void k_clear(State S)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    for (int f = l; f < CELL_STRIDE; f += 64) S.cell[(size_t)env * CELL_STRIDE + f] = -1;
+    PieceRec r;
+    r.pos = r.zero = r.dstep = r.dloc = -1;
+    r.mcount = r.aeat = r.psurv = 0;
+    r.ptype = r.dreason = -1;
+    CmRec c = {};
+    c.ldir = c.lchain = c.fstep = -1;
+    for (int p = l; p < PID_STRIDE; p += 64) {
+        S.piece[pc_idx(env, p)] = r;
+        for (int o = 0; o < 4; ++o) S.cm[cm_idx(env, o, p)] = c;
+    }
+    if (l == 0) {
+        EnvRec E = {};
+        E.winner = -1;
+        E.term = 1;
+        S.env[env] = E;
+        S.lg[env].n = 0;
+        S.lg[env].seat = 0;
+    }
+}
+
 // Start an env from a lineup (GameState.new_game, state.py:490-620; beliefs,
 // info_model.py:218-265). Zobrist includes every term new_game XORs in.
 __device__ void init_env(const State &S, int env, const int8_t *types)
@@ -618,20 +637,20 @@ __device__ void init_env(const State &S, int env, const int8_t *types)
         const int t = p < NP ? types[p] : 0;
         const bool alive = t != T_NONE && cT.home[p < NP ? p : 0] >= 0 && p < NP;
         const int h = alive ? cT.home[p] : -1;
-        S.ptype[pi] = alive ? (int8_t)t : (int8_t)-1;
-        S.pos[pi] = (int16_t)h; S.zero[pi] = (int16_t)h;
-        S.mcount[pi] = 0; S.aeat[pi] = 0; S.psurv[pi] = 0;
-        S.dreason[pi] = -1; S.dstep[pi] = -1; S.dloc[pi] = -1;
+        PieceRec r;
+        r.ptype = alive ? (int8_t)t : (int8_t)-1;
+        r.pos = (int16_t)h; r.zero = (int16_t)h;
+        r.mcount = 0; r.aeat = 0; r.psurv = 0;
+        r.dreason = -1; r.dstep = -1; r.dloc = -1;
+        S.piece[pi] = r;
         if (alive) { cell[h] = (int8_t)p; z ^= zp(S.ztab, p, t, h); }
         for (int o = 0; o < 4; ++o) {
             uint8_t code = 0;
             if (alive) code = sees_truth(o, p / 30, S.show_mode) ? (uint8_t)(1 + t - 2) : (uint8_t)(BC_PRIOR0 + p % 30);
             S.bcode[((size_t)env * 4 + o) * PID_STRIDE + p] = code;
-            const size_t ci = cm_idx(env, o, p);
-            S.cm_dlo[ci] = 0; S.cm_dhi[ci] = 0; S.cm_clo[ci] = 0; S.cm_chi[ci] = 0;
-            S.cm_elo[ci] = 0; S.cm_ehi[ci] = 0; S.cm_dtype[ci] = 0; S.cm_ctype[ci] = 0;
-            S.cm_ldir[ci] = -1; S.cm_ocnt[ci] = 0; S.cm_lchain[ci] = -1; S.cm_fstep[ci] = -1;
-            S.cm_floor[ci] = 0; S.cm_flags[ci] = 0;
+            CmRec c = {};
+            c.ldir = -1; c.lchain = -1; c.fstep = -1;
+            S.cm[cm_idx(env, o, p)] = c;
         }
     }
     z = wave_xor(z);
@@ -644,14 +663,14 @@ __device__ void init_env(const State &S, int env, const int8_t *types)
     if (l < 4) {
         uint8_t trk = 0;
         for (int s = 0; s < 4; ++s) if (s != l && ((s & 1) != (l & 1))) trk |= (uint8_t)(1u << s);
-        S.remtrk[(size_t)env * 4 + l] = trk;
+        S.env[env].remtrk[l] = trk;
     }
     if (l == 0) {
         const uint64_t *Z = S.ztab;
         z ^= Z[ZOFF_TURN + 0] ^ Z[ZOFF_MC + 0] ^ Z[ZOFF_MSLC + 0] ^ Z[ZOFF_WIN + 0] ^ Z[ZOFF_SHOW + S.show_mode];
-        S.zob[env] = z;
-        S.turn[env] = 0; S.term[env] = 0; S.winner[env] = -1; S.draw[env] = 0;
-        S.sdead[env] = 0; S.sflag[env] = 0; S.mc[env] = 0; S.mslc[env] = 0; S.hmeta[env] = 0;
+        EnvRec &W = S.env[env];
+        W.zob = z; W.mc = 0; W.mslc = 0; W.hmeta = 0;
+        W.turn = 0; W.term = 0; W.winner = -1; W.draw = 0; W.sdead = 0; W.sflag = 0;
     }
 }
 
@@ -665,7 +684,7 @@ __global__ __launch_bounds__(64) void k_reset_lineups(State S, const int8_t *__r
 __global__ __launch_bounds__(64) void k_reset_terminated(State S, int64_t seed)
 {
     const int env = blockIdx.x;
-    if (env >= S.n || !S.term[env]) return;
+    if (env >= S.n || !S.env[env].term) return;
     // pool pick of the reference reset kernel (game_state.cu:2986-2991)
     uint64_t h = (uint64_t)env * 2654435761ull + (uint64_t)seed;
     h ^= h >> 17;
@@ -684,7 +703,8 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
     uint64_t z = 0;
     for (int p = l; p < NP; p += 64) {
         const size_t pi = (size_t)env * PID_STRIDE + p;
-        const int f = S.pos[pi], t = S.ptype[pi];
+        const PieceRec r = S.piece[pi];
+        const int f = r.pos, t = r.ptype;
         if (f >= 0 && t >= 0) z ^= zp(S.ztab, p, t, f);
         for (int o = 0; o < 4 && beliefs; ++o) {
             uint8_t code = 0;
@@ -707,20 +727,21 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
     if (beliefs && l < 4) {
         uint8_t trk = 0;
         for (int s = 0; s < 4; ++s) if (s != l && ((s & 1) != (l & 1))) trk |= (uint8_t)(1u << s);
-        S.remtrk[(size_t)env * 4 + l] = trk;
+        S.env[env].remtrk[l] = trk;
     }
     if (l == 0) {
         const uint64_t *Z = S.ztab;
-        const int w = S.winner[env];
-        z ^= Z[ZOFF_TURN + S.turn[env]] ^ Z[ZOFF_MC + (S.mc[env] & 0xFFF)] ^ Z[ZOFF_MSLC + (S.mslc[env] & 0x1FF)];
-        z ^= Z[ZOFF_WIN + (w < 0 ? 0 : w + 1)] ^ Z[ZOFF_SHOW + S.show_mode];
-        if (S.term[env]) z ^= Z[ZOFF_TERM];
-        if (S.draw[env]) z ^= Z[ZOFF_DRAW];
+        const EnvRec &E = S.env[env];
+        const int w = E.winner;
+        z ^= Z[ZOFF_TURN + (E.turn & 3)] ^ Z[ZOFF_MC + (E.mc & 0xFFF)] ^ Z[ZOFF_MSLC + (E.mslc & 0x1FF)];
+        z ^= Z[ZOFF_WIN + (w < 0 ? 0 : (w & 1) + 1)] ^ Z[ZOFF_SHOW + S.show_mode];
+        if (E.term) z ^= Z[ZOFF_TERM];
+        if (E.draw) z ^= Z[ZOFF_DRAW];
         for (int s = 0; s < 4; ++s) {
-            if ((S.sdead[env] >> s) & 1) z ^= Z[ZOFF_SDEAD + s];
-            if ((S.sflag[env] >> s) & 1) z ^= Z[ZOFF_SFLAG + s];
+            if ((E.sdead >> s) & 1) z ^= Z[ZOFF_SDEAD + s];
+            if ((E.sflag >> s) & 1) z ^= Z[ZOFF_SFLAG + s];
         }
-        S.zob[env] = z;
+        S.env[env].zob = z;
     }
 }
 
@@ -736,8 +757,9 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     if (env >= S.n) return;
     __shared__ int8_t cell[CELL_STRIDE];
     __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
-    const int seat = acting ? acting[env] : S.turn[env];
-    const bool off = S.term[env] || seat < 0 || seat > 3 || ((S.sdead[env] >> (seat & 3)) & 1);
+    const EnvRec &E = S.env[env];
+    const int seat = acting ? acting[env] : E.turn;
+    const bool off = E.term || seat < 0 || seat > 3 || ((E.sdead >> (seat & 3)) & 1);
     for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
     for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
     __syncthreads();
@@ -747,8 +769,9 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     uint64_t m0 = 0, m1 = 0, m2 = 0;
     if (!off && l < 30) {
         const int pid = seat * 30 + l;
-        src = S.pos[(size_t)env * PID_STRIDE + pid];
-        const int t = S.ptype[(size_t)env * PID_STRIDE + pid];
+        const PieceRec r = S.piece[pc_idx(env, pid)];
+        src = r.pos;
+        const int t = r.ptype;
         mov = src >= 0 && t != T_JUNQI && t != T_DILEI && !is_sh(src);
         if (mov) {
             eng = t == T_GONGB;
@@ -775,9 +798,9 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     const int nmov = __popcll(__ballot(mov));
     const int total = wave_sum(mov ? cnt : 0);
     if (mov) {
-        S.lg_src[(size_t)env * 32 + rank] = (int16_t)src;
-        uint64_t *mk = S.lg_mask + ((size_t)env * 32 + rank) * 3;
-        mk[0] = m0; mk[1] = m1; mk[2] = m2;
+        LegalRec &G = S.lg[env];
+        G.src[rank] = (int16_t)src;
+        G.mask[rank][0] = m0; G.mask[rank][1] = m1; G.mask[rank][2] = m2;
         // canonical compact mask bits (gpu_rollout.py:1220-1238 layout)
         if (mask_words || mask_bool) {
             const int cs = cT.rotc[seat][cT.f2c[src]] * NONB;
@@ -794,8 +817,8 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
         }
     }
     if (l == 0) {
-        S.lg_n[env] = nmov;
-        S.lg_seat[env] = (int8_t)seat;
+        S.lg[env].n = nmov;
+        S.lg[env].seat = seat;
         if (counts) counts[env] = total;
     }
     __syncthreads();
@@ -853,13 +876,13 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
 {
     const int env = blockIdx.x, l = threadIdx.x;
     if (env >= S.n) return;
-    const int n = S.lg_n[env];
+    const LegalRec &G = S.lg[env];
+    const int n = G.n;
     int cnt = 0, src = 0;
     uint64_t m[3] = {0, 0, 0};
     if (l < n) {
-        src = S.lg_src[(size_t)env * 32 + l];
-        const uint64_t *mk = S.lg_mask + ((size_t)env * 32 + l) * 3;
-        m[0] = mk[0]; m[1] = mk[1]; m[2] = mk[2];
+        src = G.src[l];
+        m[0] = G.mask[l][0]; m[1] = G.mask[l][1]; m[2] = G.mask[l][2];
         cnt = __popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]);
     }
     int incl = cnt;

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -126,60 +127,39 @@ int dalloc(jq_env *e, T *&p, size_t count, int fill_byte)
     return JQ_OK;
 }
 
-struct FieldDesc { int elems, bytes; };
+// Where field f lives: array, per-env stride, element stride, byte offset of
+// element 0 inside its record, element size, elements per env.
+enum FieldArr { AR_CELL, AR_PIECE, AR_CM, AR_BCODE, AR_REM, AR_ENV, AR_HIST };
+struct FieldDesc { int arr, elems, bytes; size_t env_stride, el_stride, off; };
+#define PF(m) {AR_PIECE, PID_STRIDE, (int)sizeof(PieceRec::m), PID_STRIDE * sizeof(PieceRec), sizeof(PieceRec), offsetof(PieceRec, m)}
+#define CF(m) {AR_CM, 4 * PID_STRIDE, (int)sizeof(CmRec::m), 4 * PID_STRIDE * sizeof(CmRec), sizeof(CmRec), offsetof(CmRec, m)}
+#define EF(m) {AR_ENV, 1, (int)sizeof(EnvRec::m), sizeof(EnvRec), sizeof(EnvRec::m), offsetof(EnvRec, m)}
 const FieldDesc kFields[JQ_F_COUNT] = {
-    {CELL_STRIDE, 1}, {PID_STRIDE, 1}, {PID_STRIDE, 2}, {PID_STRIDE, 2}, {PID_STRIDE, 2}, {PID_STRIDE, 2},
-    {PID_STRIDE, 2}, {PID_STRIDE, 1}, {PID_STRIDE, 2}, {PID_STRIDE, 2}, {4 * PID_STRIDE, 1}, {4 * 48, 1},
-    {4, 1},
-    {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 2},
-    {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 8},
-    {4 * PID_STRIDE, 8}, {4 * PID_STRIDE, 1}, {4 * PID_STRIDE, 2}, {4 * PID_STRIDE, 1},
-    {HIST_LEN, 4}, {1, 4}, {1, 1}, {1, 1}, {1, 1}, {1, 1}, {1, 1}, {1, 1}, {1, 4}, {1, 4}, {1, 8},
+    {AR_CELL, CELL_STRIDE, 1, CELL_STRIDE, 1, 0},
+    PF(ptype), PF(pos), PF(zero), PF(mcount), PF(aeat), PF(psurv), PF(dreason), PF(dstep), PF(dloc),
+    {AR_BCODE, 4 * PID_STRIDE, 1, 4 * PID_STRIDE, 1, 0},
+    {AR_REM, 4 * 48, 1, 4 * 48, 1, 0},
+    {AR_ENV, 4, 1, sizeof(EnvRec), 1, offsetof(EnvRec, remtrk)},
+    CF(dlo), CF(dhi), CF(dtype), CF(ldir), CF(ocnt), CF(clo), CF(chi), CF(ctype), CF(lchain), CF(elo), CF(ehi),
+    CF(floor), CF(fstep), CF(flags),
+    {AR_HIST, HIST_LEN, 4, HIST_LEN * 4, 4, 0},
+    EF(hmeta), EF(turn), EF(term), EF(winner), EF(draw), EF(sdead), EF(sflag), EF(mc), EF(mslc), EF(zob),
 };
+#undef PF
+#undef CF
+#undef EF
 
-void *field_base(jq_env *e, int f)
+uint8_t *field_array(jq_env *e, int arr)
 {
     State &S = e->S;
-    switch (f) {
-    case JQ_F_CELL: return S.cell;
-    case JQ_F_PTYPE: return S.ptype;
-    case JQ_F_POS: return S.pos;
-    case JQ_F_ZERO: return S.zero;
-    case JQ_F_MOVE_COUNT: return S.mcount;
-    case JQ_F_ACTIVE_EAT: return S.aeat;
-    case JQ_F_PASSIVE_SURV: return S.psurv;
-    case JQ_F_DEATH_REASON: return S.dreason;
-    case JQ_F_DEATH_STEP: return S.dstep;
-    case JQ_F_DEATH_LOC: return S.dloc;
-    case JQ_F_BELIEF: return S.bcode;
-    case JQ_F_REMAINING: return S.rem;
-    case JQ_F_REM_TRACKED: return S.remtrk;
-    case JQ_F_CM_DIRECT_LO: return S.cm_dlo;
-    case JQ_F_CM_DIRECT_HI: return S.cm_dhi;
-    case JQ_F_CM_DIRECT_TYPE: return S.cm_dtype;
-    case JQ_F_CM_LAST_DIRECT: return S.cm_ldir;
-    case JQ_F_CM_OTHER_COUNT: return S.cm_ocnt;
-    case JQ_F_CM_CHAIN_LO: return S.cm_clo;
-    case JQ_F_CM_CHAIN_HI: return S.cm_chi;
-    case JQ_F_CM_CHAIN_TYPE: return S.cm_ctype;
-    case JQ_F_CM_LAST_CHAIN: return S.cm_lchain;
-    case JQ_F_CM_EATEN_LO: return S.cm_elo;
-    case JQ_F_CM_EATEN_HI: return S.cm_ehi;
-    case JQ_F_CM_FLOOR: return S.cm_floor;
-    case JQ_F_CM_FLOOR_STEP: return S.cm_fstep;
-    case JQ_F_CM_FLAGS: return S.cm_flags;
-    case JQ_F_HIST: return S.hist;
-    case JQ_F_HIST_META: return S.hmeta;
-    case JQ_F_TURN: return S.turn;
-    case JQ_F_TERMINATED: return S.term;
-    case JQ_F_WINNER: return S.winner;
-    case JQ_F_DRAW: return S.draw;
-    case JQ_F_SEAT_DEAD: return S.sdead;
-    case JQ_F_FLAG_REV: return S.sflag;
-    case JQ_F_MOVE_COUNTER: return S.mc;
-    case JQ_F_MSLC: return S.mslc;
-    case JQ_F_ZOBRIST: return S.zob;
-    default: return nullptr;
+    switch (arr) {
+    case AR_CELL: return reinterpret_cast<uint8_t *>(S.cell);
+    case AR_PIECE: return reinterpret_cast<uint8_t *>(S.piece);
+    case AR_CM: return reinterpret_cast<uint8_t *>(S.cm);
+    case AR_BCODE: return S.bcode;
+    case AR_REM: return reinterpret_cast<uint8_t *>(S.rem);
+    case AR_ENV: return reinterpret_cast<uint8_t *>(S.env);
+    default: return reinterpret_cast<uint8_t *>(S.hist);
     }
 }
 
@@ -243,26 +223,19 @@ int jq_create(jq_env **out, int32_t n, int32_t max_num_moves, int32_t show_mode,
     const size_t N = (size_t)n;
 #define A(ptr, cnt, fill) do { if ((rc = dalloc(e, ptr, cnt, fill)) != 0) { jq_destroy(e); return rc; } } while (0)
     A(S.cell, N * CELL_STRIDE, 0xFF);
-    A(S.ptype, N * PID_STRIDE, 0xFF);
-    A(S.pos, N * PID_STRIDE, 0xFF);
-    A(S.zero, N * PID_STRIDE, 0xFF);
-    A(S.mcount, N * PID_STRIDE, 0); A(S.aeat, N * PID_STRIDE, 0); A(S.psurv, N * PID_STRIDE, 0);
-    A(S.dreason, N * PID_STRIDE, 0xFF); A(S.dstep, N * PID_STRIDE, 0xFF); A(S.dloc, N * PID_STRIDE, 0xFF);
+    A(S.piece, N * PID_STRIDE, 0);
+    A(S.cm, N * 4 * PID_STRIDE, 0);
     A(S.bcode, N * 4 * PID_STRIDE, 0);
     A(S.rem, N * 4 * 48, 0);
-    A(S.remtrk, N * 4, 0);
-    const size_t C = N * 4 * PID_STRIDE;
-    A(S.cm_dlo, C, 0); A(S.cm_dhi, C, 0); A(S.cm_clo, C, 0); A(S.cm_chi, C, 0); A(S.cm_elo, C, 0); A(S.cm_ehi, C, 0);
-    A(S.cm_dtype, C, 0); A(S.cm_ctype, C, 0);
-    A(S.cm_ldir, C, 0xFF); A(S.cm_ocnt, C, 0); A(S.cm_lchain, C, 0xFF); A(S.cm_fstep, C, 0xFF);
-    A(S.cm_floor, C, 0); A(S.cm_flags, C, 0);
-    A(S.hist, N * HIST_LEN, 0); A(S.hmeta, N, 0);
-    A(S.turn, N, 0); A(S.term, N, 0); A(S.winner, N, 0xFF); A(S.draw, N, 0);
-    A(S.sdead, N, 0); A(S.sflag, N, 0); A(S.mc, N, 0); A(S.mslc, N, 0); A(S.zob, N, 0);
-    A(S.lg_src, N * 32, 0); A(S.lg_mask, N * 32 * 3, 0); A(S.lg_n, N, 0); A(S.lg_seat, N, 0);
+    A(S.env, N, 0);
+    A(S.hist, N * HIST_LEN, 0);
+    A(S.lg, N, 0);
     A(e->tmp_actions, N, 0);
     uint64_t *zt = nullptr; A(zt, (size_t)ZTOTAL, 0); S.ztab = zt;
     float *rl = nullptr; A(rl, 4 * 4096, 0); S.rlut = rl;
+    hipLaunchKernelGGL(k_clear, dim3(n), dim3(64), 0, 0, S);
+    if ((rc = launch_check("k_clear")) != 0) { jq_destroy(e); return rc; }
+    if (hipDeviceSynchronize() != hipSuccess) { jq_destroy(e); return fail(JQ_E_HIP, "state clear failed"); }
 #undef A
     *out = e;
     return JQ_OK;
@@ -484,8 +457,16 @@ int jq_get_field(jq_env *e, int32_t f, void *host)
     int rc = check_env(e);
     if (rc) return rc;
     if (f < 0 || f >= JQ_F_COUNT || !host) return fail(JQ_E_ARG, "bad field %d", f);
+    const FieldDesc &d = kFields[f];
+    const size_t n = (size_t)e->S.n;
+    std::vector<uint8_t> tmp(n * d.env_stride);
     HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipMemcpy(host, field_base(e, f), (size_t)e->S.n * kFields[f].elems * kFields[f].bytes, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(tmp.data(), field_array(e, d.arr), tmp.size(), hipMemcpyDeviceToHost));
+    uint8_t *out = static_cast<uint8_t *>(host);
+    for (size_t i = 0; i < n; ++i)
+        for (int j = 0; j < d.elems; ++j)
+            std::memcpy(out + (i * d.elems + j) * d.bytes, tmp.data() + i * d.env_stride + j * d.el_stride + d.off,
+                        d.bytes);
     return JQ_OK;
 }
 
@@ -494,15 +475,28 @@ int jq_set_field(jq_env *e, int32_t f, const void *host)
     int rc = check_env(e);
     if (rc) return rc;
     if (f < 0 || f >= JQ_F_COUNT || !host) return fail(JQ_E_ARG, "bad field %d", f);
+    const FieldDesc &d = kFields[f];
+    const size_t n = (size_t)e->S.n;
+    std::vector<uint8_t> tmp(n * d.env_stride);
     HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipMemcpy(field_base(e, f), host, (size_t)e->S.n * kFields[f].elems * kFields[f].bytes, hipMemcpyHostToDevice));
+    uint8_t *base = field_array(e, d.arr);
+    HIP_TRY(hipMemcpy(tmp.data(), base, tmp.size(), hipMemcpyDeviceToHost));
+    const uint8_t *in = static_cast<const uint8_t *>(host);
+    for (size_t i = 0; i < n; ++i)
+        for (int j = 0; j < d.elems; ++j)
+            std::memcpy(tmp.data() + i * d.env_stride + j * d.el_stride + d.off, in + (i * d.elems + j) * d.bytes,
+                        d.bytes);
+    HIP_TRY(hipMemcpy(base, tmp.data(), tmp.size(), hipMemcpyHostToDevice));
     return JQ_OK;
 }
 
-int jq_field_ptr(jq_env *e, int32_t f, void **ptr)
+int jq_field_ptr(jq_env *e, int32_t f, void **ptr, int64_t *env_stride, int64_t *el_stride)
 {
     if (!e || !ptr || f < 0 || f >= JQ_F_COUNT) return fail(JQ_E_ARG, "bad field %d", f);
-    *ptr = field_base(e, f);
+    const FieldDesc &d = kFields[f];
+    *ptr = field_array(e, d.arr) + d.off;
+    if (env_stride) *env_stride = (int64_t)d.env_stride;
+    if (el_stride) *el_stride = (int64_t)d.el_stride;
     return JQ_OK;
 }
 

@@ -152,26 +152,27 @@ struct PieceIn {
 __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int pid, PieceIn &P)
 {
     const int le = (obs + 1) & 3, re = (obs + 3) & 3, s = pid / 30;
-    const size_t pi = (size_t)env * PID_STRIDE + pid;
-    P.pos = S.pos[pi]; P.tp = S.ptype[pi];
-    P.mcount = S.mcount[pi]; P.aeat = S.aeat[pi]; P.psurv = S.psurv[pi];
-    P.dstep = S.dstep[pi]; P.dreason = S.dreason[pi]; P.dloc = S.dloc[pi]; P.zero = S.zero[pi];
+    const PieceRec r = S.piece[pc_idx(env, pid)];
+    P.pos = r.pos; P.tp = r.ptype;
+    P.mcount = r.mcount; P.aeat = r.aeat; P.psurv = r.psurv;
+    P.dstep = r.dstep; P.dreason = r.dreason; P.dloc = r.dloc; P.zero = r.zero;
     P.bcode = S.bcode[((size_t)env * 4 + obs) * PID_STRIDE + pid];
-    const size_t ci = cm_idx(env, obs, pid);
     P.dlo = P.dhi = P.clo = P.chi = P.elo = P.ehi = P.ldlo = P.ldhi = P.rdlo = P.rdhi = 0;
     P.dtype = P.ctype = P.ocnt = P.floor = P.flags = 0;
     P.ldir = P.lchain = P.fstep = -1;
     P.locnt = P.rocnt = P.lflags = P.rflags = 0;
     if ((s & 1) != (obs & 1)) {
-        P.dlo = S.cm_dlo[ci]; P.dhi = S.cm_dhi[ci]; P.clo = S.cm_clo[ci]; P.chi = S.cm_chi[ci];
-        P.dtype = S.cm_dtype[ci]; P.ctype = S.cm_ctype[ci]; P.ocnt = S.cm_ocnt[ci];
-        P.floor = S.cm_floor[ci]; P.flags = S.cm_flags[ci];
-        P.ldir = S.cm_ldir[ci]; P.lchain = S.cm_lchain[ci]; P.fstep = S.cm_fstep[ci];
+        const CmRec c = S.cm[cm_idx(env, obs, pid)];
+        P.dlo = c.dlo; P.dhi = c.dhi; P.clo = c.clo; P.chi = c.chi;
+        P.dtype = c.dtype; P.ctype = c.ctype; P.ocnt = c.ocnt;
+        P.floor = c.floor; P.flags = c.flags;
+        P.ldir = c.ldir; P.lchain = c.lchain; P.fstep = c.fstep;
     } else if (s == obs) {
-        P.elo = S.cm_elo[ci]; P.ehi = S.cm_ehi[ci];
-        const size_t li = cm_idx(env, le, pid), ri = cm_idx(env, re, pid);
-        P.ldlo = S.cm_dlo[li]; P.ldhi = S.cm_dhi[li]; P.locnt = S.cm_ocnt[li]; P.lflags = S.cm_flags[li];
-        P.rdlo = S.cm_dlo[ri]; P.rdhi = S.cm_dhi[ri]; P.rocnt = S.cm_ocnt[ri]; P.rflags = S.cm_flags[ri];
+        const CmRec &c = S.cm[cm_idx(env, obs, pid)];
+        P.elo = c.elo; P.ehi = c.ehi;
+        const CmRec &lc = S.cm[cm_idx(env, le, pid)], &rc = S.cm[cm_idx(env, re, pid)];
+        P.ldlo = lc.dlo; P.ldhi = lc.dhi; P.locnt = lc.ocnt; P.lflags = lc.flags;
+        P.rdlo = rc.dlo; P.rdhi = rc.dhi; P.rocnt = rc.ocnt; P.rflags = rc.flags;
     }
 }
 
@@ -299,7 +300,7 @@ __device__ __forceinline__ int row_env(int row, int all_seats) { return all_seat
 __device__ __forceinline__ int row_obs(const State &S, const int8_t *observer, int all_seats, int row)
 {
     if (all_seats) return (observer ? observer[row] : row) & 3;
-    return (observer ? observer[row] : S.turn[row]) & 3;
+    return (observer ? observer[row] : S.env[row].turn) & 3;
 }
 
 // Seat of the observer's i-th relation in plane order: self, teammate, left, right.
@@ -307,27 +308,28 @@ __device__ __forceinline__ int seat_rel(int obs, int i) { return (obs + (i == 0 
 
 __device__ void row_load(const State &S, int env, int obs, int t, RowIn &R)
 {
-    R.mc = S.mc[env];
-    R.mslc = S.mslc[env];
-    R.ptype = t < PID_STRIDE ? S.ptype[(size_t)env * PID_STRIDE + t] : -1;
+    const EnvRec &E = S.env[env];   // uniform: scalar loads
+    R.mc = E.mc;
+    R.mslc = E.mslc;
+    R.ptype = t < PID_STRIDE ? S.piece[pc_idx(env, t)].ptype : -1;
     R.hist = 0; R.hmeta = 0; R.flag_on = 0;
     if (t < NP) {
         piece_load(S, env, obs, t, R.P);
     } else if (t >= T_HIST && t < T_FLAGS) {
         R.hist = S.hist[(size_t)env * HIST_LEN + (t - T_HIST)];
-        R.hmeta = S.hmeta[env];
+        R.hmeta = E.hmeta;
     } else if (t >= T_FLAGS && t < T_END) {
         const int j = t - T_FLAGS;
-        R.flag_on = j < 3 ? ((S.sdead[env] >> seat_rel(obs, j + 1)) & 1) : ((S.sflag[env] >> seat_rel(obs, j - 3)) & 1);
+        R.flag_on = j < 3 ? ((E.sdead >> seat_rel(obs, j + 1)) & 1) : ((E.sflag >> seat_rel(obs, j - 3)) & 1);
     }
     R.gval = 0.f;
     if (t < 24) {   // remaining counts of the left / right enemy (observation.py:1623-1651)
         const int seat = t < 12 ? (obs + 1) & 3 : (obs + 3) & 3;
-        const bool trk = (S.remtrk[(size_t)env * 4 + obs] >> seat) & 1;
+        const bool trk = (E.remtrk[obs] >> seat) & 1;
         const int cnt = S.rem[((size_t)env * 4 + obs) * 48 + seat * 12 + t % 12];
         R.gval = trk ? (float)cnt : 0.f;
     } else if (t < 28) {   // flag_revealed of self, teammate, left, right
-        R.gval = (float)((S.sflag[env] >> seat_rel(obs, t - 24)) & 1);
+        R.gval = (float)((E.sflag >> seat_rel(obs, t - 24)) & 1);
     }
 }
 
