@@ -89,6 +89,16 @@ struct State {
     const int8_t *pool;    // [pool_size][120]
 };
 
+// Block barrier that orders LDS only. __syncthreads() is a workgroup fence over
+// all address spaces, which also waits for every outstanding global store of
+// the wave; a kernel that streams stores across LDS phases must not pay that.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ size_t cm_idx(int env, int o, int pid) { return ((size_t)env * 4 + o) * PID_STRIDE + pid; }
 __device__ __forceinline__ size_t pc_idx(int env, int pid) { return (size_t)env * PID_STRIDE + pid; }
 

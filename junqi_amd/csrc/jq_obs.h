@@ -344,7 +344,7 @@ __device__ void obs_setup(ObsLds &L)
         L.decb[t] = f32_to_bf16_rne(d);
     }
     if (t < STAT_NQ * 4) L.stat[t] = 0;
-    __syncthreads();
+    lds_barrier();
     for (int k = t; k < NC; k += OBS_THREADS) {   // board_static (58-63): fixed cell classes
         uint32_t sm = cT.statics[k];
         while (sm) {
@@ -356,7 +356,7 @@ __device__ void obs_setup(ObsLds &L)
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 __device__ __forceinline__ float recency_at(const State &S, int mc, int last, int q)
@@ -397,7 +397,7 @@ __device__ void obs_build(const State &S, int obs, int m, const RowIn &R, ObsLds
         double mp = (double)R.mc / 4000.0; if (mp > 1.0) mp = 1.0;
         L.turnv[0] = (float)dp; L.turnv[1] = (float)mp;
     }
-    __syncthreads();
+    lds_barrier();
     if (t < NP) {
         piece_scatter(S, obs, t, m, R.P, rc, L);
     } else if (t < PID_STRIDE) {
@@ -422,7 +422,7 @@ __device__ void obs_build(const State &S, int obs, int m, const RowIn &R, ObsLds
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Code of element e (0 <= e < OBS_ROW).
@@ -566,27 +566,87 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m)
     if (threadIdx.x == 64 && ((NBYTES + lead) & 15)) obs_elems<FMT>(L, row, ql * EPC - m, OBS_ROW, m);
 }
 
-// The six continuous planes of the u8 format as float32 (N, 6, 17, 17).
+// Image offset of the u8 chunk starting at element e0: inside the range it
+// overlaps (ranges are more than 16 elements apart, so at most one), else the
+// always-zero word. Branch-free per lane.
+__device__ __forceinline__ int u8_img_off(int e0, int d0, int d1, int d2, int d3)
+{
+    int off = IMG_ZERO;
+    off = (e0 < RG0_E && e0 + 16 > RG0_S) ? e0 + d0 : off;
+    off = (e0 < RG1_E && e0 + 16 > RG1_S) ? e0 + d1 : off;
+    off = (e0 < RG2_E && e0 + 16 > RG2_S) ? e0 + d2 : off;
+    off = (e0 < RG3_E && e0 + 16 > RG3_S) ? e0 + d3 : off;
+    return off;
+}
+
+__device__ __forceinline__ uint4 u8_chunk(const ObsLds &L, int e0, int off)
+{
+    const uint32_t v = bit_window(L, e0);
+    const uint4 b = *reinterpret_cast<const uint4 *>(&L.img[off]);
+    return make_uint4(nib_to_bytes(v) | b.x, nib_to_bytes(v >> 4) | b.y, nib_to_bytes(v >> 8) | b.z,
+                      nib_to_bytes(v >> 12) | b.w);
+}
+
+// Aux element e of a row: planes 64, 65 (turn history) then 253..256 (recency).
+__device__ __forceinline__ float aux_at(const ObsLds &L, int e)
+{
+    const int j = e / NC, k = e - j * NC;
+    return obs_cont_at(L, j < 2 ? 64 + j : 251 + j, k);
+}
+
+__device__ __forceinline__ uint4 aux_chunk(const ObsLds &L, int e0)
+{
+    return make_uint4(__float_as_uint(aux_at(L, e0)), __float_as_uint(aux_at(L, e0 + 1)),
+                      __float_as_uint(aux_at(L, e0 + 2)), __float_as_uint(aux_at(L, e0 + 3)));
+}
+
+// The six continuous planes of a u8 row as float32 (6, 17, 17): one 16-byte
+// chunk per thread per iteration over the whole block.
 __device__ void obs_emit_aux(const ObsLds &L, float *row)
 {
-    const uintptr_t B = (uintptr_t)row;
-    const uintptr_t A0 = B & ~(uintptr_t)15;
-    const uintptr_t E = B + (uintptr_t)AUX_ROW * 4;
-    const int nchunks = (int)((E - A0 + 15) >> 4);
-    for (int q = threadIdx.x; q < nchunks; q += OBS_THREADS) {
-        const uintptr_t A = A0 + (uintptr_t)q * 16;
-        const uintptr_t lo = A < B ? B : A, hi = A + 16 > E ? E : A + 16;
-        uint32_t w[4] = {0, 0, 0, 0};
-        for (uintptr_t p = lo; p < hi; p += 4) {
-            const int e = (int)((p - B) / 4);
-            const int j = e / NC, k = e - j * NC;
-            w[(p - A) >> 2] = __float_as_uint(obs_cont_at(L, j < 2 ? 64 + j : 251 + j, k));
-        }
-        if (lo == A && hi == A + 16)
-            *reinterpret_cast<uint4 *>(row + (ptrdiff_t)(A - B) / 4) = make_uint4(w[0], w[1], w[2], w[3]);
-        else
-            for (uintptr_t p = lo; p < hi; p += 4) row[(p - B) / 4] = __uint_as_float(w[(p - A) >> 2]);
+    const int lead = (int)(((uintptr_t)row >> 2) & 3);          // elements before the first 16-byte line
+    const int qf = lead ? 1 : 0, ql = (AUX_ROW + lead) >> 2;    // full chunks [qf, ql)
+    for (int q = qf + (int)threadIdx.x; q < ql; q += OBS_THREADS) {
+        const int e0 = q * 4 - lead;
+        *reinterpret_cast<uint4 *>(row + e0) = aux_chunk(L, e0);
     }
+    if (threadIdx.x == 128) for (int e = 0; e < (lead ? 4 - lead : 0); ++e) row[e] = aux_at(L, e);
+    if (threadIdx.x == 192) for (int e = ql * 4 - lead; e < AUX_ROW; ++e) row[e] = aux_at(L, e);
+}
+
+// u8 row emission: the row's full 16-byte chunks are split into contiguous
+// ranges, one per wave; a lane writes two chunks per iteration (the wave covers
+// 2 KB), so two independent LDS -> expand -> store chains overlap. The aux
+// planes follow, spread over the block.
+__device__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m, float *aux)
+{
+    const int lead = m;
+    const int qf = lead ? 1 : 0, ql = (OBS_ROW + lead) >> 4;   // full chunks [qf, ql)
+    const int d0 = RG0_B + 16 + ((RG0_S + m) & 15) - RG0_S, d1 = RG1_B + 16 + ((RG1_S + m) & 15) - RG1_S;
+    const int d2 = RG2_B + 16 + ((RG2_S + m) & 15) - RG2_S, d3 = RG3_B + 16 + ((RG3_S + m) & 15) - RG3_S;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    constexpr int NW = OBS_THREADS / 64;
+    const int nq = ql - qf;
+    const int fair = (nq + NW - 1) / NW;
+    const int per = ((fair + 64) / 128) * 128;                  // whole 2 KB steps, nearest to fair
+    const int wa = min(ql, qf + wv * per), wb = wv == NW - 1 ? ql : min(ql, wa + per);
+    for (int qb = wa; qb < wb; qb += 128) {
+        const int q0 = qb + lane, q1 = q0 + 64;
+        const int e0 = q0 * 16 - m, e1 = q1 * 16 - m;
+        if (q1 < wb) {
+            const uint4 a = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
+            const uint4 b = u8_chunk(L, e1, u8_img_off(e1, d0, d1, d2, d3));
+            *reinterpret_cast<uint4 *>(row + e0) = a;
+            *reinterpret_cast<uint4 *>(row + e1) = b;
+        } else if (q0 < wb) {
+            *reinterpret_cast<uint4 *>(row + e0) = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
+        }
+    }
+    // partial chunks at the two ends of the row
+    if (threadIdx.x == 0 && lead) obs_elems<2>(L, row, 0, 16 - m, m);
+    if (threadIdx.x == 64 && ((OBS_ROW + lead) & 15)) obs_elems<2>(L, row, ql * 16 - m, OBS_ROW, m);
+    if (aux) obs_emit_aux(L, aux);
 }
 
 // nrows = N (one row per env, observer given or the acting seat) or 4N
@@ -620,11 +680,11 @@ __global__ __launch_bounds__(OBS_THREADS) __attribute__((amdgpu_waves_per_eu(4, 
             row_load(S, row_env(nrow, all_seats), obs_next, t, R);
             if (nrow + G < nrows) obs_after = row_obs(S, observer, all_seats, nrow + G);
         }
-        obs_emit<FMT>(L, rowp, m);
-        if (FMT == 2 && aux) obs_emit_aux(L, aux + (size_t)row * AUX_ROW);
+        if (FMT == 2) obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUX_ROW : nullptr);
+        else obs_emit<FMT>(L, rowp, m);
         if (glob && t < 28) glob[(size_t)row * 28 + t] = gv;
         if (!more) break;
-        __syncthreads();   // the LDS row is rebuilt next
+        lds_barrier();   // the LDS row is rebuilt next
         row = nrow;
         obs = obs_next;
         obs_next = obs_after;
