@@ -99,6 +99,10 @@ def cpu_baseline(envs: int, steps: int) -> dict:
                       f"random legal actions, HALF_DARK"}
 
 
+# device kernel that writes the observation rows, per output format
+OBS_KERNEL = {"f32": "jq::k_observe<0>", "bf16": "jq::k_observe<1>", "u8": "jq::k_observe_u8_persist"}
+
+
 def measured_traffic(kernel: str, games: int):
     """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, scaled against a
     plain copy) from the committed counter summary, when it was taken at this size."""
@@ -198,8 +202,8 @@ def main() -> int:
                    "mean_legal_actions": round(kbar, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(f"jq::k_observe<{ {'f32': 0, 'bf16': 1, 'u8': 2}[args.fmt] }>", n),
-                     "kernel": f"k_observe<{args.fmt}>", "kernel_ms": round(obs_ms, 4),
+                     "traffic": measured_traffic(OBS_KERNEL[args.fmt], n),
+                     "kernel": OBS_KERNEL[args.fmt], "kernel_ms": round(obs_ms, 4),
                      "bytes_per_launch": obs_bytes},
         "wall_s": round(wall, 3),
     }

@@ -848,26 +848,48 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     }
 }
 
-// Exclusive scan of counts into offsets (N+1); one block.
-__global__ __launch_bounds__(1024) void k_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets, int n)
+// Exclusive scan of counts into offsets (N+1); one 1024-thread block walks the
+// array in tiles of 4096: coalesced int4 loads (4 envs per thread), a wave scan
+// by shuffles, the 16 wave totals scanned through LDS, and a carry between tiles.
+constexpr int SCAN_THREADS = 1024, SCAN_TILE = 4 * SCAN_THREADS;
+__global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+                                                      int n)
 {
-    __shared__ int32_t part[1024];
-    const int t = threadIdx.x;
-    const int per = (n + 1023) / 1024;
-    const int b = t * per, e = min(n, b + per);
-    int s = 0;
-    for (int i = b; i < e; ++i) s += counts[i];
-    part[t] = s;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int v = t >= o ? part[t - o] : 0;
+    __shared__ int32_t wsum[SCAN_THREADS / 64];
+    __shared__ int32_t carry_s;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    int carry = 0;
+    for (int base = 0; base < n; base += SCAN_TILE) {
+        const int i0 = base + 4 * t;
+        int v[4];
+        if (i0 + 3 < n && ((reinterpret_cast<uintptr_t>(counts + i0) & 15) == 0)) {
+            const int4 c = *reinterpret_cast<const int4 *>(counts + i0);
+            v[0] = c.x; v[1] = c.y; v[2] = c.z; v[3] = c.w;
+        } else {
+            for (int k = 0; k < 4; ++k) v[k] = i0 + k < n ? counts[i0 + k] : 0;
+        }
+        const int tsum = v[0] + v[1] + v[2] + v[3];
+        int incl = tsum;
+        for (int o = 1; o < 64; o <<= 1) { const int u = __shfl_up(incl, o); if (lane >= o) incl += u; }
+        if (lane == 63) wsum[w] = incl;
         __syncthreads();
-        part[t] += v;
+        if (w == 0) {
+            const int x = lane < SCAN_THREADS / 64 ? wsum[lane] : 0;
+            int y = x;
+            for (int o = 1; o < SCAN_THREADS / 64; o <<= 1) { const int u = __shfl_up(y, o); if (lane >= o) y += u; }
+            if (lane < SCAN_THREADS / 64) wsum[lane] = y - x;   // exclusive wave prefix
+            if (lane == SCAN_THREADS / 64 - 1) carry_s = y;      // tile total
+        }
+        __syncthreads();
+        int run = carry + wsum[w] + incl - tsum;
+        for (int k = 0; k < 4; ++k) {
+            if (i0 + k < n) offsets[i0 + k] = run;
+            run += v[k];
+        }
+        carry += carry_s;
         __syncthreads();
     }
-    int run = t ? part[t - 1] : 0;
-    for (int i = b; i < e; ++i) { offsets[i] = run; run += counts[i]; }
-    if (t == 1023) offsets[n] = part[1023];
+    if (t == 0) offsets[n] = carry;
 }
 
 // Write each env's ids at its offset: pieces in ascending source order, each

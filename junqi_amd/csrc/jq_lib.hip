@@ -26,7 +26,7 @@ struct jq_env {
     std::vector<void *> allocs;
     bool zob_ready = false, rlut_ready = false;
     int32_t *tmp_actions = nullptr;
-    int obs_blocks[3] = {0, 0, 0};   // resident k_observe blocks on the device, per format
+    int obs_blocks = 0;              // resident u8 observation blocks on the device
 };
 
 namespace {
@@ -179,21 +179,16 @@ int launch_check(const char *what)
     return JQ_OK;
 }
 
-// Persistent grid of k_observe<FMT>: every block the device can hold at once.
-template <int FMT>
-int obs_grid_fmt(jq_env *e)
+// Persistent grid of the u8 observation kernel: every block the device can
+// hold at once.
+int obs_u8_grid(jq_env *e)
 {
+    if (e->obs_blocks > 0) return JQ_OK;
     int per_cu = 0, cus = 0;
-    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_observe<FMT>, OBS_THREADS, 0));
+    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_observe_u8_persist, OBS_THREADS, 0));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
-    e->obs_blocks[FMT] = std::max(1, per_cu) * std::max(1, cus);
+    e->obs_blocks = std::max(1, per_cu) * std::max(1, cus);
     return JQ_OK;
-}
-
-int obs_grid(jq_env *e, int fmt)
-{
-    if (e->obs_blocks[fmt] > 0) return JQ_OK;
-    return fmt == 0 ? obs_grid_fmt<0>(e) : fmt == 1 ? obs_grid_fmt<1>(e) : obs_grid_fmt<2>(e);
 }
 
 }  // namespace
@@ -245,6 +240,7 @@ int jq_destroy(jq_env *e)
 {
     if (!e) return JQ_OK;
     (void)hipSetDevice(e->device);
+
     for (void *p : e->allocs) (void)hipFree(p);
     delete e;
     return JQ_OK;
@@ -368,7 +364,7 @@ int jq_legal(jq_env *e, const int8_t *acting, int32_t *counts, int32_t *offsets,
     hipLaunchKernelGGL(k_legal, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, acting, counts, mask_words, mask_bool);
     if ((rc = launch_check("k_legal")) != 0) return rc;
     if (offsets) {
-        hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, strm(stream), counts, offsets, e->S.n);
+        hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, strm(stream), counts, offsets, e->S.n);
         if ((rc = launch_check("k_scan")) != 0) return rc;
     }
     if (values) {
@@ -390,14 +386,16 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
         return fail(JQ_E_ARG, "observation buffers must be aligned to their element size");
     if ((fmt != JQ_OBS_U8 || aux) && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
     const int nrows = all_seats ? e->S.n * 4 : e->S.n;
-    if ((rc = obs_grid(e, fmt)) != 0) return rc;
-    // u8 rows stream fast enough that the next row's gathers need hiding: persistent
-    // blocks prefetch them. The wider formats run one row per block.
-    const dim3 grid(fmt == JQ_OBS_U8 ? std::min(nrows, e->obs_blocks[fmt]) : nrows), block(OBS_THREADS);
+    const dim3 grid(nrows), block(OBS_THREADS);
     switch (fmt) {
     case JQ_OBS_F32: hipLaunchKernelGGL(k_observe<0>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
     case JQ_OBS_BF16: hipLaunchKernelGGL(k_observe<1>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
-    default: hipLaunchKernelGGL(k_observe<2>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
+    default:
+        if ((rc = obs_u8_grid(e)) != 0) return rc;
+        hipLaunchKernelGGL(k_observe_u8_persist, dim3(std::min(nrows, e->obs_blocks)), dim3(OBS_THREADS), 0,
+                           strm(stream), e->S, observer, all_seats, static_cast<uint8_t *>(spatial), aux, global,
+                           nrows);
+        break;
     }
     return launch_check("k_observe");
 }
@@ -429,6 +427,7 @@ int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_
 {
     int rc = check_env(e);
     if (rc) return rc;
+    if (!counts || !offsets || !values) return fail(JQ_E_ARG, "env_step needs counts, offsets and values");
     const int32_t *act = actions;
     if (!act) {
         int32_t *dst = actions_out ? actions_out : e->tmp_actions;
@@ -439,6 +438,8 @@ int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_
                       nullptr, reward, nullptr, stream)) != 0)
         return rc;
     if (e->S.pool && (rc = jq_reset_terminated(e, reset_seed, stream)) != 0) return rc;
+    // sequential on purpose: the u8 observation grid holds every CU's LDS, so a
+    // concurrent legal-action launch only slows both down
     if ((rc = jq_legal(e, nullptr, counts, offsets, values, mask_words, nullptr, stream)) != 0) return rc;
     if (spatial && (rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream)) != 0) return rc;
     return JQ_OK;

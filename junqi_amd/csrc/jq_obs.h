@@ -21,9 +21,10 @@
 // The six continuous planes (turn history, recency) are exact floats: they go
 // to the aux output in the u8 format and are computed per element in f32 / bf16.
 //
-// Blocks are persistent (grid = resident blocks): while a block streams row i
-// out, its threads already hold the loads of row i + gridDim.x in registers,
-// so the gather latency of the next build hides behind the current stores.
+// The u8 kernel is persistent (grid = resident blocks): while a block streams
+// row i out, its threads already hold the gathered inputs of row i + gridDim.x
+// in registers, so the next fill only waits for the recency-table lookups.
+// f32 / bf16 rows are 2-4x wider; they run one 256-thread block per row.
 #pragma once
 
 namespace jq {
@@ -70,10 +71,7 @@ struct ObsLds {
     float rec[PID_STRIDE][4];        // recency values per pid (0 unless an enemy piece on board)
     float dec[32];                   // code -> f32
     uint32_t decb[32];               // code -> bf16 bits
-    int32_t hist[HIST_LEN];          // move-history ring as stored
-    int32_t hmeta;
     int8_t cpid[CELL_STRIDE];        // canonical cell -> pid (-1 empty)
-    int8_t ptype[PID_STRIDE];        // piece type per pid
     uint8_t bval[BC_COUNT * 12 + 4]; // belief row code x type -> value code
     float turnv[2];
 };
@@ -177,7 +175,8 @@ __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int
 }
 
 // Scatter one pid's nonzero elements into bits / img.
-__device__ void piece_scatter(const State &S, int obs, int pid, int m, const PieceIn &P, const float rc[4], ObsLds &L)
+__device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, int m, const PieceIn &P,
+                                              const float rc[4], const uint32_t own_types[4], ObsLds &L)
 {
     const int tm = (obs + 2) & 3, le = (obs + 1) & 3, team = obs & 1;
     const int s = pid / 30;
@@ -191,7 +190,7 @@ __device__ void piece_scatter(const State &S, int obs, int pid, int m, const Pie
         if (rel == 0 && P.tp >= 2 && P.tp <= 13) set_el(L, (P.tp - 2) * NC + k);
         if (rel == 2) set_el(L, 25 * NC + k);
         if (rel == 3) set_el(L, 26 * NC + k);
-        if (rel == 1 && S.show_mode == SM_DARK) set_el(L, 24 * NC + k);
+        if (rel == 1 && show_mode == SM_DARK) set_el(L, 24 * NC + k);
         // beliefs (12-23 teammate, 27-38 left, 39-50 right)
         if (rel != 0) {
             const int bc = P.bcode < BC_COUNT ? P.bcode : 0;
@@ -235,7 +234,8 @@ __device__ void piece_scatter(const State &S, int obs, int pid, int m, const Pie
             for (uint32_t hits = seat_bits(P.dlo, P.dhi, obs * 30); hits; hits &= hits - 1) {
                 const int sl = __builtin_ctz(hits);
                 set_el(L, (223 + sl) * NC + k);
-                const int gt = L.ptype[obs * 30 + sl];
+                const uint32_t tw = sl < 8 ? own_types[0] : sl < 16 ? own_types[1] : sl < 24 ? own_types[2] : own_types[3];
+                const int gt = (tw >> ((sl & 7) * 4)) & 15;   // the killed piece's type
                 if (gt >= 2 && gt <= 13) tcnt += 1ull << (5 * (gt - 2));
             }
 #pragma unroll 1
@@ -282,16 +282,6 @@ __device__ void piece_scatter(const State &S, int obs, int pid, int m, const Pie
 }
 
 
-// One thread's inputs of a row, loaded ahead of the build that uses them.
-struct RowIn {
-    PieceIn P;      // t < NP
-    int ptype;      // t < PID_STRIDE
-    int hist, hmeta;  // T_HIST <= t < T_FLAGS: ring slot t - T_HIST
-    int flag_on;    // T_FLAGS <= t < T_END
-    int mc, mslc;
-    float gval;     // t < 28: the row's global feature t
-};
-
 __device__ __forceinline__ int row_env(int row, int all_seats) { return all_seats ? row >> 2 : row; }
 
 // Observer of a row: all_seats rows take observer[env * 4 + k] (k-th slot of the
@@ -306,38 +296,19 @@ __device__ __forceinline__ int row_obs(const State &S, const int8_t *observer, i
 // Seat of the observer's i-th relation in plane order: self, teammate, left, right.
 __device__ __forceinline__ int seat_rel(int obs, int i) { return (obs + (i == 0 ? 0 : i == 1 ? 2 : i == 2 ? 1 : 3)) & 3; }
 
-__device__ void row_load(const State &S, int env, int obs, int t, RowIn &R)
-{
-    const EnvRec &E = S.env[env];   // uniform: scalar loads
-    R.mc = E.mc;
-    R.mslc = E.mslc;
-    R.ptype = t < PID_STRIDE ? S.piece[pc_idx(env, t)].ptype : -1;
-    R.hist = 0; R.hmeta = 0; R.flag_on = 0;
-    if (t < NP) {
-        piece_load(S, env, obs, t, R.P);
-    } else if (t >= T_HIST && t < T_FLAGS) {
-        R.hist = S.hist[(size_t)env * HIST_LEN + (t - T_HIST)];
-        R.hmeta = E.hmeta;
-    } else if (t >= T_FLAGS && t < T_END) {
-        const int j = t - T_FLAGS;
-        R.flag_on = j < 3 ? ((E.sdead >> seat_rel(obs, j + 1)) & 1) : ((E.sflag >> seat_rel(obs, j - 3)) & 1);
-    }
-    R.gval = 0.f;
-    if (t < 24) {   // remaining counts of the left / right enemy (observation.py:1623-1651)
-        const int seat = t < 12 ? (obs + 1) & 3 : (obs + 3) & 3;
-        const bool trk = (E.remtrk[obs] >> seat) & 1;
-        const int cnt = S.rem[((size_t)env * 4 + obs) * 48 + seat * 12 + t % 12];
-        R.gval = trk ? (float)cnt : 0.f;
-    } else if (t < 28) {   // flag_revealed of self, teammate, left, right
-        R.gval = (float)((E.sflag >> seat_rel(obs, t - 24)) & 1);
-    }
+__device__ __forceinline__ float recency_at(const State &S, int mc, int last, int q)
+{   // exp(-elapsed / tau) from the table (observation.py:1545-1567)
+    if (last < 0) return 0.f;
+    int el = mc - last;
+    el = el < 0 ? 0 : (el > 4095 ? 4095 : el);
+    return S.rlut[q * 4096 + el];
 }
 
-// Row-independent LDS content, once per block.
-__device__ void obs_setup(ObsLds &L)
+// Row-independent LDS content (tables, board_static template) of one buffer.
+// All `nthreads` threads of the block call it; it ends with a barrier.
+__device__ __forceinline__ void obs_setup(ObsLds &L, int t, int nthreads)
 {
-    const int t = threadIdx.x;
-    for (int i = t; i < BC_COUNT * 12; i += OBS_THREADS) L.bval[i] = cBVAL[i / 12][i % 12];
+    for (int i = t; i < BC_COUNT * 12; i += nthreads) L.bval[i] = cBVAL[i / 12][i % 12];
     if (t < 32) {
         const float d = t < 17 ? cDECODE[t] : 0.f;
         L.dec[t] = d;
@@ -345,7 +316,7 @@ __device__ void obs_setup(ObsLds &L)
     }
     if (t < STAT_NQ * 4) L.stat[t] = 0;
     lds_barrier();
-    for (int k = t; k < NC; k += OBS_THREADS) {   // board_static (58-63): fixed cell classes
+    for (int k = t; k < NC; k += nthreads) {   // board_static (58-63): fixed cell classes
         uint32_t sm = cT.statics[k];
         while (sm) {
             const int b = __builtin_ctz(sm);
@@ -359,62 +330,101 @@ __device__ void obs_setup(ObsLds &L)
     lds_barrier();
 }
 
-__device__ __forceinline__ float recency_at(const State &S, int mc, int last, int q)
-{   // exp(-elapsed / tau) from the table (observation.py:1545-1567)
-    if (last < 0) return 0.f;
-    int el = mc - last;
-    el = el < 0 ? 0 : (el > 4095 ? 4095 : el);
-    return S.rlut[q * 4096 + el];
+// Empty row: zero bits except the board_static template, zero image, no pieces.
+// Thread t of `nthreads`.
+__device__ __forceinline__ void obs_clear(ObsLds &L, int t, int nthreads)
+{
+    uint4 *w = reinterpret_cast<uint4 *>(L.bits);
+    const uint4 *st = reinterpret_cast<const uint4 *>(L.stat);
+    for (int i = t; i < OBS_BITS_WORDS / 4; i += nthreads)
+        w[i] = (unsigned)(i - STAT_Q0) < (unsigned)STAT_NQ ? st[i - STAT_Q0] : make_uint4(0, 0, 0, 0);
+    uint4 *b = reinterpret_cast<uint4 *>(L.img);
+    for (int i = t; i < IMG_BYTES / 16; i += nthreads) b[i] = make_uint4(0, 0, 0, 0);
+    for (int k = t; k < CELL_STRIDE; k += nthreads) L.cpid[k] = -1;
 }
 
-// Build the LDS form of row (env, obs) from R; m is the row's element phase.
-__device__ void obs_build(const State &S, int obs, int m, const RowIn &R, ObsLds &L)
+// Producer thread -> pid, grouped by relation so each wave runs one code path:
+// wave 0 = own (t 0-29) and teammate (30-59) pieces, wave 1 = left (64-93) and
+// right (94-123) enemies. -1 for the threads in between.
+__device__ __forceinline__ int piece_of_thread(int t, int obs)
 {
-    const int t = threadIdx.x;
-    float rc[4] = {0.f, 0.f, 0.f, 0.f};   // gathered first: the latency overlaps the clears
-    if (t < NP && (unsigned)R.P.pos < (unsigned)NC && ((t / 30) & 1) != (obs & 1)) {
-        rc[0] = recency_at(S, R.mc, R.P.ldir, 0);
-        rc[1] = recency_at(S, R.mc, R.P.ldir, 1);
-        rc[2] = recency_at(S, R.mc, R.P.lchain, 2);
-        rc[3] = recency_at(S, R.mc, R.P.fstep, 3);
+    if (t < 30) return obs * 30 + t;
+    if (t < 60) return ((obs + 2) & 3) * 30 + (t - 30);
+    if (t >= 64 && t < 94) return ((obs + 1) & 3) * 30 + (t - 64);
+    if (t >= 94 && t < 124) return ((obs + 3) & 3) * 30 + (t - 94);
+    return -1;
+}
+
+// One producer thread's inputs of a row (thread roles below), everything that
+// depends only on (env, observer): gathered in one round of independent loads.
+struct RowIn {
+    PieceIn P;              // t < NP
+    uint32_t own_types[4];  // the observer's 30 piece types, 4 bits each
+    int hist;               // T_HIST <= t < T_FLAGS: ring slot t - T_HIST as stored
+    int mc, mslc, hmeta;
+    int sdead, sflag, remtrk;
+    int rem;                // t < 24: remaining count behind global feature t
+};
+
+// Thread roles: 0..127 one pid each (piece_of_thread) or, for the 8 spare
+// threads, one padding recency slot; 128..159 one move-history ring slot each,
+// 160..166 the whole-plane seat flags; 0..27 also write the 28 globals.
+__device__ __forceinline__ void row_fetch(const State &S, int env, int obs, int t, RowIn &R)
+{
+    const EnvRec &E = S.env[env];   // uniform: scalar loads
+    R.mc = E.mc; R.mslc = E.mslc; R.hmeta = E.hmeta;
+    R.sdead = E.sdead; R.sflag = E.sflag; R.remtrk = E.remtrk[obs];
+    for (int w = 0; w < 4; ++w) {
+        uint32_t v = 0;
+        for (int j = 0; j < 8 && w * 8 + j < 30; ++j)
+            v |= (uint32_t)(S.piece[pc_idx(env, obs * 30 + w * 8 + j)].ptype & 15) << (4 * j);
+        R.own_types[w] = v;
     }
-    {
-        uint4 *w = reinterpret_cast<uint4 *>(L.bits);
-        const uint4 *st = reinterpret_cast<const uint4 *>(L.stat);
-        for (int i = t; i < OBS_BITS_WORDS / 4; i += OBS_THREADS)
-            w[i] = (unsigned)(i - STAT_Q0) < (unsigned)STAT_NQ ? st[i - STAT_Q0] : make_uint4(0, 0, 0, 0);
-        uint4 *b = reinterpret_cast<uint4 *>(L.img);
-        for (int i = t; i < IMG_BYTES / 16; i += OBS_THREADS) b[i] = make_uint4(0, 0, 0, 0);
+    R.hist = 0;
+    R.rem = 0;
+    const int pid = t < PID_STRIDE ? piece_of_thread(t, obs) : -1;
+    if (pid >= 0) piece_load(S, env, obs, pid, R.P);
+    else if (t >= T_HIST && t < T_FLAGS) R.hist = S.hist[(size_t)env * HIST_LEN + (t - T_HIST)];
+    if (t < 24) {
+        const int seat = t < 12 ? (obs + 1) & 3 : (obs + 3) & 3;
+        R.rem = S.rem[((size_t)env * 4 + obs) * 48 + seat * 12 + t % 12];
     }
-    for (int k = t; k < CELL_STRIDE; k += OBS_THREADS) L.cpid[k] = -1;
-    if (t < PID_STRIDE) L.ptype[t] = (int8_t)R.ptype;
-    if (t >= T_HIST && t < T_FLAGS) {
-        L.hist[t - T_HIST] = R.hist;
-        if (t == T_HIST) L.hmeta = R.hmeta;
-    }
-    if (t == 0) {   // turn_history: float64 divide, then rounded to float32 (observation.py:1000-1021)
-        double dp = (double)R.mslc / 200.0; if (dp > 1.0) dp = 1.0;
-        double mp = (double)R.mc / 4000.0; if (mp > 1.0) mp = 1.0;
-        L.turnv[0] = (float)dp; L.turnv[1] = (float)mp;
-    }
-    lds_barrier();
-    if (t < NP) {
-        piece_scatter(S, obs, t, m, R.P, rc, L);
-    } else if (t < PID_STRIDE) {
-        for (int q = 0; q < 4; ++q) L.rec[t][q] = 0.f;
+}
+
+// Fill a cleared buffer with row (env, obs) from the fetched inputs, thread t
+// in [0, 256). Only the recency-table gathers are loads here. No thread reads
+// what another one writes, so no barrier is needed inside.
+__device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, const RowIn &R, ObsLds &L,
+                                         float *glob_row)
+{
+    const int pid = t < PID_STRIDE ? piece_of_thread(t, obs) : -1;
+    if (pid >= 0) {
+        float rc[4] = {0.f, 0.f, 0.f, 0.f};
+        if ((unsigned)R.P.pos < (unsigned)NC && t >= 64) {   // enemy pieces on the board
+            rc[0] = recency_at(S, R.mc, R.P.ldir, 0);
+            rc[1] = recency_at(S, R.mc, R.P.ldir, 1);
+            rc[2] = recency_at(S, R.mc, R.P.lchain, 2);
+            rc[3] = recency_at(S, R.mc, R.P.fstep, 3);
+        }
+        piece_scatter(S.show_mode, obs, pid, m, R.P, rc, R.own_types, L);
+    } else if (t < PID_STRIDE) {   // the 8 spare threads clear the padding pids' recency
+        const int pad = NP + (t < 64 ? t - 60 : t - 120);
+        for (int q = 0; q < 4; ++q) L.rec[pad][q] = 0.f;
     } else if (t < T_FLAGS) {   // move_history (129-160), observation.py:1207-1231
-        const int d = t - T_HIST;
-        const int cnt = L.hmeta & 0xFF, head = (L.hmeta >> 8) & 31;
+        const int cnt = R.hmeta & 0xFF, head = (R.hmeta >> 8) & 31;
+        const int d = (head - 1 - (t - T_HIST)) & 31;   // plane of this ring slot (0 = most recent)
         if (d < cnt) {
-            const int e = L.hist[(head - 1 - d) & 31];
+            const int e = R.hist;
             const int hs = canon_cell(obs, min(e & 0xFFFF, NC - 1));
             const int hd = canon_cell(obs, min((e >> 16) & 0xFFFF, NC - 1));
             if (hs != hd) set_code(L, RG2_B, RG2_S, (129 + d) * NC + hs, m, CODE_NEG);
             set_code(L, RG2_B, RG2_S, (129 + d) * NC + hd, m, CODE_ONE);
         }
     } else if (t < T_END) {   // whole planes: dead_flags 51-53, flag_revealed 54-57
-        if (R.flag_on) {
-            const int e0 = (51 + t - T_FLAGS) * NC, e1 = e0 + NC;
+        const int j = t - T_FLAGS;
+        const bool on = j < 3 ? ((R.sdead >> seat_rel(obs, j + 1)) & 1) : ((R.sflag >> seat_rel(obs, j - 3)) & 1);
+        if (on) {
+            const int e0 = (51 + j) * NC, e1 = e0 + NC;
             for (int w = e0 >> 5; w <= (e1 - 1) >> 5; ++w) {
                 const int lo = max(e0, w * 32) - w * 32, hi = min(e1, w * 32 + 32) - w * 32;
                 const uint32_t mask = (hi - lo == 32) ? 0xFFFFFFFFu : (((1u << (hi - lo)) - 1u) << lo);
@@ -422,7 +432,21 @@ __device__ void obs_build(const State &S, int obs, int m, const RowIn &R, ObsLds
             }
         }
     }
-    lds_barrier();
+    if (t == 0) {   // turn_history: float64 divide, then rounded to float32 (observation.py:1000-1021)
+        double dp = (double)R.mslc / 200.0; if (dp > 1.0) dp = 1.0;
+        double mp = (double)R.mc / 4000.0; if (mp > 1.0) mp = 1.0;
+        L.turnv[0] = (float)dp; L.turnv[1] = (float)mp;
+    }
+    if (glob_row && t < 28) {   // globals (observation.py:1623-1651)
+        float v;
+        if (t < 24) {   // remaining counts of the left / right enemy
+            const int seat = t < 12 ? (obs + 1) & 3 : (obs + 3) & 3;
+            v = ((R.remtrk >> seat) & 1) ? (float)R.rem : 0.f;
+        } else {   // flag_revealed of self, teammate, left, right
+            v = (float)((R.sflag >> seat_rel(obs, t - 24)) & 1);
+        }
+        glob_row[t] = v;
+    }
 }
 
 // Code of element e (0 <= e < OBS_ROW).
@@ -506,7 +530,7 @@ __device__ __forceinline__ uint4 obs_chunk(const ObsLds &L, int e0, int off, boo
 
 // Elements [e, f) of the row written one by one (row ends, continuous planes).
 template <int FMT>
-__device__ void obs_elems(const ObsLds &L, uint8_t *row, int e, int f, int m)
+__device__ __forceinline__ void obs_elems(const ObsLds &L, uint8_t *row, int e, int f, int m)
 {
     for (; e < f; ++e) {
         const uint32_t v = obs_elem<FMT>(L, e, m);
@@ -602,92 +626,98 @@ __device__ __forceinline__ uint4 aux_chunk(const ObsLds &L, int e0)
 
 // The six continuous planes of a u8 row as float32 (6, 17, 17): one 16-byte
 // chunk per thread per iteration over the whole block.
-__device__ void obs_emit_aux(const ObsLds &L, float *row)
+__device__ __forceinline__ void obs_emit_aux(const ObsLds &L, float *row, int ct)
 {
     const int lead = (int)(((uintptr_t)row >> 2) & 3);          // elements before the first 16-byte line
     const int qf = lead ? 1 : 0, ql = (AUX_ROW + lead) >> 2;    // full chunks [qf, ql)
-    for (int q = qf + (int)threadIdx.x; q < ql; q += OBS_THREADS) {
+    for (int q = qf + ct; q < ql; q += OBS_THREADS) {
         const int e0 = q * 4 - lead;
         *reinterpret_cast<uint4 *>(row + e0) = aux_chunk(L, e0);
     }
-    if (threadIdx.x == 128) for (int e = 0; e < (lead ? 4 - lead : 0); ++e) row[e] = aux_at(L, e);
-    if (threadIdx.x == 192) for (int e = ql * 4 - lead; e < AUX_ROW; ++e) row[e] = aux_at(L, e);
+    if (ct == 128) for (int e = 0; e < (lead ? 4 - lead : 0); ++e) row[e] = aux_at(L, e);
+    if (ct == 192) for (int e = ql * 4 - lead; e < AUX_ROW; ++e) row[e] = aux_at(L, e);
 }
 
 // u8 row emission: the row's full 16-byte chunks are split into contiguous
 // ranges, one per wave; a lane writes two chunks per iteration (the wave covers
 // 2 KB), so two independent LDS -> expand -> store chains overlap. The aux
 // planes follow, spread over the block.
-__device__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m, float *aux)
+__device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m, float *aux, int ct)
 {
     const int lead = m;
     const int qf = lead ? 1 : 0, ql = (OBS_ROW + lead) >> 4;   // full chunks [qf, ql)
     const int d0 = RG0_B + 16 + ((RG0_S + m) & 15) - RG0_S, d1 = RG1_B + 16 + ((RG1_S + m) & 15) - RG1_S;
     const int d2 = RG2_B + 16 + ((RG2_S + m) & 15) - RG2_S, d3 = RG3_B + 16 + ((RG3_S + m) & 15) - RG3_S;
-    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(ct >> 6);
+    const int lane = ct & 63;
     constexpr int NW = OBS_THREADS / 64;
     const int nq = ql - qf;
     const int fair = (nq + NW - 1) / NW;
     const int per = ((fair + 64) / 128) * 128;                  // whole 2 KB steps, nearest to fair
     const int wa = min(ql, qf + wv * per), wb = wv == NW - 1 ? ql : min(ql, wa + per);
-    for (int qb = wa; qb < wb; qb += 128) {
-        const int q0 = qb + lane, q1 = q0 + 64;
-        const int e0 = q0 * 16 - m, e1 = q1 * 16 - m;
-        if (q1 < wb) {
-            const uint4 a = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
-            const uint4 b = u8_chunk(L, e1, u8_img_off(e1, d0, d1, d2, d3));
-            *reinterpret_cast<uint4 *>(row + e0) = a;
-            *reinterpret_cast<uint4 *>(row + e1) = b;
-        } else if (q0 < wb) {
-            *reinterpret_cast<uint4 *>(row + e0) = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
-        }
+    // chunk q covers row bytes [q*16 - m, q*16 - m + 16): a 16-byte aligned slot
+    // of the output, indexed from the aligned address below the row start
+    uint4 *__restrict__ slot = reinterpret_cast<uint4 *>(__builtin_assume_aligned(row - m, 16));
+    for (int q = wa + lane; q < wb; q += 64) {
+        const int e0 = q * 16 - m;
+        slot[q] = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
     }
     // partial chunks at the two ends of the row
-    if (threadIdx.x == 0 && lead) obs_elems<2>(L, row, 0, 16 - m, m);
-    if (threadIdx.x == 64 && ((OBS_ROW + lead) & 15)) obs_elems<2>(L, row, ql * 16 - m, OBS_ROW, m);
-    if (aux) obs_emit_aux(L, aux);
+    if (ct == 0 && lead) obs_elems<2>(L, row, 0, 16 - m, m);
+    if (ct == 64 && ((OBS_ROW + lead) & 15)) obs_elems<2>(L, row, ql * 16 - m, OBS_ROW, m);
+    if (aux) obs_emit_aux(L, aux, ct);
 }
 
 // nrows = N (one row per env, observer given or the acting seat) or 4N
-// (all_seats: row = env * 4 + observer). Launched with at most the number of
-// co-resident blocks; block b handles rows b, b + gridDim.x, ...
+// (all_seats: row = env * 4 + observer). One 256-thread block per row.
 template <int FMT>
-__global__ __launch_bounds__(OBS_THREADS) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_observe(State S, const int8_t *__restrict__ observer, int all_seats,
+__global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *__restrict__ observer, int all_seats,
                                                          void *__restrict__ spatial, float *__restrict__ aux,
                                                          float *__restrict__ glob, int nrows)
 {
     __shared__ ObsLds L;
     constexpr int ES = FMT == 0 ? 4 : FMT == 1 ? 2 : 1;
-    const int t = threadIdx.x;
-    const int G = gridDim.x;
-    int row = blockIdx.x;
+    const int t = threadIdx.x, row = blockIdx.x;
     if (row >= nrows) return;
-    obs_setup(L);
+    const int env = row_env(row, all_seats), obs = row_obs(S, observer, all_seats, row);
+    uint8_t *rowp = reinterpret_cast<uint8_t *>(spatial) + (size_t)row * OBS_ROW * ES;
+    const int m = (int)(((uintptr_t)rowp / ES) & (16 / ES - 1));
+    obs_setup(L, t, OBS_THREADS);
+    obs_clear(L, t, OBS_THREADS);
+    lds_barrier();
     RowIn R;
-    int obs = row_obs(S, observer, all_seats, row);
-    row_load(S, row_env(row, all_seats), obs, t, R);
-    int obs_next = row + G < nrows ? row_obs(S, observer, all_seats, row + G) : 0;
-    for (;;) {
-        uint8_t *rowp = reinterpret_cast<uint8_t *>(spatial) + (size_t)row * OBS_ROW * ES;
-        const int m = (int)(((uintptr_t)rowp / ES) & (16 / ES - 1));
-        obs_build(S, obs, m, R, L);
-        const float gv = R.gval;
-        const int nrow = row + G;
-        const bool more = nrow < nrows;
-        int obs_after = 0;
-        if (more) {   // next row's loads are in flight while this row streams out
-            row_load(S, row_env(nrow, all_seats), obs_next, t, R);
-            if (nrow + G < nrows) obs_after = row_obs(S, observer, all_seats, nrow + G);
-        }
-        if (FMT == 2) obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUX_ROW : nullptr);
-        else obs_emit<FMT>(L, rowp, m);
-        if (glob && t < 28) glob[(size_t)row * 28 + t] = gv;
-        if (!more) break;
-        lds_barrier();   // the LDS row is rebuilt next
-        row = nrow;
-        obs = obs_next;
-        obs_next = obs_after;
+    row_fetch(S, env, obs, t, R);
+    row_fill(S, obs, m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr);
+    lds_barrier();
+    if (FMT == 2) obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUX_ROW : nullptr, t);
+    else obs_emit<FMT>(L, rowp, m);
+}
+
+// u8, persistent single-buffer form: 256 threads, one LDS row. Per row: fill
+// from the inputs fetched during the previous row, fetch the next row's inputs
+// (in flight during the stores), stream the row, clear the buffer.
+__global__ __launch_bounds__(OBS_THREADS) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_observe_u8_persist(
+    State S, const int8_t *__restrict__ observer, int all_seats, uint8_t *__restrict__ spatial,
+    float *__restrict__ aux, float *__restrict__ glob, int nrows)
+{
+    __shared__ ObsLds L;
+    const int t = threadIdx.x, G = gridDim.x;
+    if ((int)blockIdx.x >= nrows) return;   // uniform per block
+    obs_setup(L, t, OBS_THREADS);
+    obs_clear(L, t, OBS_THREADS);
+    RowIn R;
+    row_fetch(S, row_env(blockIdx.x, all_seats), row_obs(S, observer, all_seats, blockIdx.x), t, R);
+    lds_barrier();
+    for (int row = blockIdx.x; row < nrows; row += G) {
+        uint8_t *rowp = spatial + (size_t)row * OBS_ROW;
+        const int m = (int)((uintptr_t)rowp & 15);
+        row_fill(S, row_obs(S, observer, all_seats, row), m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr);
+        lds_barrier();
+        if (row + G < nrows) row_fetch(S, row_env(row + G, all_seats), row_obs(S, observer, all_seats, row + G), t, R);
+        obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUX_ROW : nullptr, t);
+        lds_barrier();
+        obs_clear(L, t, OBS_THREADS);
+        lds_barrier();
     }
 }
 
