@@ -109,6 +109,191 @@ __device__ void engineer_mask(const int8_t *cell, int src, int team, uint64_t &m
     m0 = wave_or(p0); m1 = wave_or(p1); m2 = wave_or(p2);
 }
 
+// ------------------------------------------------------------------ bitboards
+// 129-bit sets over compact cells (bit c = compact cell c), three words.
+struct BB {
+    uint64_t w0, w1, w2;
+};
+__device__ __forceinline__ bool bb_has(const BB &b, int c)
+{
+    const uint64_t w = c < 64 ? b.w0 : c < 128 ? b.w1 : b.w2;
+    return (w >> (c & 63)) & 1ull;
+}
+__device__ __forceinline__ BB bb_and(const BB &a, const BB &b) { return {a.w0 & b.w0, a.w1 & b.w1, a.w2 & b.w2}; }
+__device__ __forceinline__ BB bb_or(const BB &a, const BB &b) { return {a.w0 | b.w0, a.w1 | b.w1, a.w2 | b.w2}; }
+__device__ __forceinline__ bool bb_any(const BB &b) { return (b.w0 | b.w1 | b.w2) != 0; }
+__device__ __forceinline__ int bb_lowest(const BB &b)
+{
+    return b.w0 ? __builtin_ctzll(b.w0) : b.w1 ? 64 + __builtin_ctzll(b.w1) : 128 + __builtin_ctzll(b.w2);
+}
+__device__ __forceinline__ int bb_highest(const BB &b)
+{
+    return b.w2 ? 191 - __builtin_clzll(b.w2) : b.w1 ? 127 - __builtin_clzll(b.w1) : 63 - __builtin_clzll(b.w0);
+}
+__device__ __forceinline__ uint64_t lowmask(int n)
+{   // bits [0, n) of a word, n clamped to [0, 64]
+    return n <= 0 ? 0ull : n >= 64 ? ~0ull : (1ull << n) - 1ull;
+}
+__device__ __forceinline__ BB bb_below(int c) { return {lowmask(c), lowmask(c - 64), lowmask(c - 128)}; }
+__device__ __forceinline__ BB bb_above(int c) { return {~lowmask(c + 1), ~lowmask(c - 63), ~lowmask(c - 127)}; }
+
+// Number of set bits of the 289-bit flat mask m below bit f (0 <= f < 289):
+// with m = on-board cells this is f's compact index, with m = rail cells its
+// rail index. The masks are uniform, so they sit in scalar registers.
+__device__ __forceinline__ int flat_rank(const uint64_t m[5], int f)
+{
+    int n = 0;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) n += __popcll(m[k] & lowmask(f - 64 * k));
+    return n;
+}
+__device__ __forceinline__ bool flat_has(const uint64_t m[5], int f)
+{
+    const int k = f >> 6;
+    const uint64_t w = k == 0 ? m[0] : k == 1 ? m[1] : k == 2 ? m[2] : k == 3 ? m[3] : m[4];
+    return (w >> (f & 63)) & 1ull;
+}
+
+// Occupied cells and cells holding an enemy of `team` that may be attacked
+// (not in a camp) of the env whose board is `cell` (flat, LDS). Uniform.
+__device__ __forceinline__ void env_boards(const int8_t *cell, int team, BB &occ, BB &ea)
+{
+    const int l = lane_id();
+    const int p0 = cell[cT.c2f[l]], p1 = cell[cT.c2f[l + 64]], p2 = l == 0 ? cell[cT.c2f[128]] : -1;
+    occ = {__ballot(p0 >= 0), __ballot(p1 >= 0), __ballot(p2 >= 0)};
+    const BB en = {__ballot(p0 >= 0 && team_of(p0) != team), __ballot(p1 >= 0 && team_of(p1) != team),
+                   __ballot(p2 >= 0 && team_of(p2) != team)};
+    ea = {en.w0 & ~cT.campm[0], en.w1 & ~cT.campm[1], en.w2 & ~cT.campm[2]};
+}
+
+// Road steps and, for non-engineers on a rail, straight runs and curve runs of
+// the piece on compact cell sc (rail index r or -1); lane-local
+// (move_gen.py:1052-1199 parts a, b, c, e). land = empty or attackable.
+__device__ __forceinline__ BB piece_moves_bb(int sc, int r, bool engineer, const BB &occ, const BB &ea)
+{
+    const BB land = {~occ.w0 | ea.w0, ~occ.w1 | ea.w1, (~occ.w2 | ea.w2) & 1ull};
+    BB m = {0, 0, 0};
+    const uint64_t nb8 = *reinterpret_cast<const uint64_t *>(cT.adjc[sc]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = (int)((nb8 >> (8 * j)) & 0xFF);
+        if (c != 0xFF && bb_has(land, c)) setbit3(m.w0, m.w1, m.w2, c);
+    }
+    if (engineer || r < 0) return m;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const BB run = {cT.raym[r][k][0], cT.raym[r][k][1], cT.raym[r][k][2]};
+        const BB blk = bb_and(run, occ);
+        if (!bb_any(blk)) {
+            m = bb_or(m, run);
+        } else {   // cells before the first occupied one, plus that one if attackable
+            const int f = (k & 1) ? bb_highest(blk) : bb_lowest(blk);
+            m = bb_or(m, bb_and(run, (k & 1) ? bb_above(f) : bb_below(f)));
+            if (bb_has(ea, f)) setbit3(m.w0, m.w1, m.w2, f);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const uint4 q = *reinterpret_cast<const uint4 *>(cT.crayc[r][d]);
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        bool open = true;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            const int c = (int)((qw[i >> 2] >> (8 * (i & 3))) & 0xFF);
+            if (!open || c == 0xFF) { open = false; continue; }
+            if (!bb_has(occ, c)) { setbit3(m.w0, m.w1, m.w2, c); continue; }
+            if (bb_has(ea, c)) setbit3(m.w0, m.w1, m.w2, c);
+            open = false;
+        }
+    }
+    return m;
+}
+
+// Half h (0 or 1) of the lane-local moves of piece_moves_bb, so two lanes
+// share one piece: neighbours 4h .. 4h + 3 of adjc, the +x / -x (h = 0) or
+// +y / -y (h = 1) straight runs, and curve run h. The union of both halves is
+// piece_moves_bb.
+__device__ __forceinline__ BB piece_moves_half(int sc, int r, bool engineer, int h, const BB &occ, const BB &ea)
+{
+    const BB land = {~occ.w0 | ea.w0, ~occ.w1 | ea.w1, (~occ.w2 | ea.w2) & 1ull};
+    BB m = {0, 0, 0};
+    const uint32_t nb4 = reinterpret_cast<const uint32_t *>(cT.adjc[sc])[h];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = (int)((nb4 >> (8 * j)) & 0xFF);
+        if (c != 0xFF && bb_has(land, c)) setbit3(m.w0, m.w1, m.w2, c);
+    }
+    if (engineer || r < 0) return m;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {   // k = 2h + j; j = 0 runs toward higher compact indices
+        const int k = 2 * h + j;
+        const BB run = {cT.raym[r][k][0], cT.raym[r][k][1], cT.raym[r][k][2]};
+        const BB blk = bb_and(run, occ);
+        if (!bb_any(blk)) {
+            m = bb_or(m, run);
+        } else {   // cells before the first occupied one, plus that one if attackable
+            const int f = j ? bb_highest(blk) : bb_lowest(blk);
+            m = bb_or(m, bb_and(run, j ? bb_above(f) : bb_below(f)));
+            if (bb_has(ea, f)) setbit3(m.w0, m.w1, m.w2, f);
+        }
+    }
+    const uint4 q = *reinterpret_cast<const uint4 *>(cT.crayc[r][h]);
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    bool open = true;
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+        const int c = (int)((qw[i >> 2] >> (8 * (i & 3))) & 0xFF);
+        if (!open || c == 0xFF) { open = false; continue; }
+        if (!bb_has(occ, c)) { setbit3(m.w0, m.w1, m.w2, c); continue; }
+        if (bb_has(ea, c)) setbit3(m.w0, m.w1, m.w2, c);
+        open = false;
+    }
+    return m;
+}
+
+// Rail destinations of up to three engineers at once (move_gen.py:870-895):
+// lane j < ne gets, in m, the landable rail nodes adjacent to the closure of
+// engineer j's source (rail index sr, held by lane j) through empty rail
+// nodes. Lane v evaluates rail nodes v and v + 64 each hop.
+__device__ __forceinline__ void engineers_bb(int ne, const int sr[3], const BB &occ, const BB &ea, BB out[3])
+{
+    const int l = lane_id(), v1 = l + 64;
+    const bool has1 = v1 < NRAIL;
+    const int c0 = cT.railc[l], c1 = has1 ? cT.railc[v1] : 0;
+    const bool e0 = !bb_has(occ, c0), e1 = has1 && !bb_has(occ, c1);
+    const bool l0 = e0 || bb_has(ea, c0), l1 = has1 && (e1 || bb_has(ea, c1));   // landable (empty or attackable)
+    const uint64_t a0 = cT.rnbr[l][0], a1 = cT.rnbr[l][1];
+    const uint64_t b0 = has1 ? cT.rnbr[v1][0] : 0ull, b1 = has1 ? cT.rnbr[v1][1] : 0ull;
+    uint64_t r0[3], r1[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        r0[j] = j < ne && sr[j] < 64 ? 1ull << sr[j] : 0ull;
+        r1[j] = j < ne && sr[j] >= 64 ? 1ull << (sr[j] - 64) : 0ull;
+    }
+    for (int hop = 0; hop < NRAIL; ++hop) {
+        uint64_t grew = 0;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const bool n0 = e0 && !((r0[j] >> l) & 1) && (((a0 & r0[j]) | (a1 & r1[j])) != 0);
+            const bool n1 = e1 && !((r1[j] >> (v1 & 63)) & 1) && (((b0 & r0[j]) | (b1 & r1[j])) != 0);
+            const uint64_t g0 = __ballot(n0), g1 = __ballot(n1) & 0x1FFull;
+            r0[j] |= g0;
+            r1[j] |= g1;
+            grew |= g0 | g1;
+        }
+        if (!grew) break;
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        BB p = {0, 0, 0};
+        const bool d0 = l != sr[j] && l0 && (((a0 & r0[j]) | (a1 & r1[j])) != 0);
+        const bool d1 = has1 && v1 != sr[j] && l1 && (((b0 & r0[j]) | (b1 & r1[j])) != 0);
+        if (d0) setbit3(p.w0, p.w1, p.w2, c0);
+        if (d1) setbit3(p.w0, p.w1, p.w2, c1);
+        out[j] = {wave_or(p.w0), wave_or(p.w1), wave_or(p.w2)};
+    }
+}
+
 // Road steps and (for non-engineers) straight rays and curve runs of one piece,
 // computed by the calling lane alone (move_gen.py:1052-1199 parts a, b, c, e).
 __device__ void piece_mask_lane(const int8_t *cell, int src, int team, bool engineer,
@@ -757,36 +942,60 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     if (env >= S.n) return;
     __shared__ int8_t cell[CELL_STRIDE];
     __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
+    __shared__ uint8_t rotl[NONB + 3];   // world compact -> canonical compact of the acting seat
     const EnvRec &E = S.env[env];
     const int seat = acting ? acting[env] : E.turn;
     const bool off = E.term || seat < 0 || seat > 3 || ((E.sdead >> (seat & 3)) & 1);
     for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
     for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
+    if (mask_words || mask_bool) {
+        const int s4 = seat & 3;
+        for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[s4][c];
+    }
     __syncthreads();
     const int team = seat & 1;
+    BB occ, ea;
+    env_boards(cell, team, occ, ea);
+    // lanes p and p + 32 share piece p (p < 30), one half of its moves each
+    const int h = l >> 5, p = l & 31;
     bool mov = false, eng = false;
-    int src = -1;
+    int src = -1, ridx = -1;
     uint64_t m0 = 0, m1 = 0, m2 = 0;
-    if (!off && l < 30) {
-        const int pid = seat * 30 + l;
+    if (!off && p < 30) {
+        const int pid = seat * 30 + p;
         const PieceRec r = S.piece[pc_idx(env, pid)];
         src = r.pos;
         const int t = r.ptype;
-        mov = src >= 0 && t != T_JUNQI && t != T_DILEI && !is_sh(src);
+        mov = (unsigned)src < (unsigned)NC && t != T_JUNQI && t != T_DILEI && !flat_has(cT.shm, src);
         if (mov) {
             eng = t == T_GONGB;
-            piece_mask_lane(cell, src, team, eng, m0, m1, m2);
+            const int sc = flat_rank(cT.onm, src);
+            ridx = flat_has(cT.railm, src) ? flat_rank(cT.railm, src) : -1;
+            const BB m = piece_moves_half(sc, ridx, eng, h, occ, ea);
+            m0 = m.w0; m1 = m.w1; m2 = m.w2;
         }
     }
-    uint64_t engs = __ballot(mov && eng && is_rail(src < 0 ? 0 : src));
+    m0 |= (uint64_t)__shfl_xor((long long)m0, 32);
+    m1 |= (uint64_t)__shfl_xor((long long)m1, 32);
+    m2 |= (uint64_t)__shfl_xor((long long)m2, 32);
+    // engineers on a rail, three at a time (a seat has at most three)
+    uint64_t engs = __ballot(mov && eng && ridx >= 0 && h == 0);
     while (engs) {
-        const int e = __builtin_ctzll(engs);
-        engs &= engs - 1;
-        const int esrc = __shfl(src, e);
-        uint64_t e0, e1, e2;
-        engineer_mask(cell, esrc, team, e0, e1, e2);
-        if (l == e) { m0 |= e0; m1 |= e1; m2 |= e2; }
+        int lanes[3], sr[3], ne = 0;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            lanes[j] = engs ? __builtin_ctzll(engs) : 64;
+            ne += engs ? 1 : 0;
+            engs &= engs - 1;
+            sr[j] = lanes[j] < 64 ? __shfl(ridx, lanes[j]) : -1;
+        }
+        BB em[3];
+        engineers_bb(ne, sr, occ, ea, em);
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            if (p == lanes[j]) { m0 |= em[j].w0; m1 |= em[j].w1; m2 |= em[j].w2; }
     }
+    const bool lead = mov && h == 0;   // the lane that reports piece p
     const int cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
     // rank of this piece's source cell among the movable pieces
     int rank = 0;
@@ -795,24 +1004,26 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
         const bool mj = __shfl((int)mov, j) != 0;
         rank += (mov && mj && oj < src) ? 1 : 0;
     }
-    const int nmov = __popcll(__ballot(mov));
-    const int total = wave_sum(mov ? cnt : 0);
-    if (mov) {
+    const int nmov = __popcll(__ballot(lead));
+    const int total = wave_sum(lead ? cnt : 0);
+    if (lead) {
         LegalRec &G = S.lg[env];
         G.src[rank] = (int16_t)src;
         G.mask[rank][0] = m0; G.mask[rank][1] = m1; G.mask[rank][2] = m2;
-        // canonical compact mask bits (gpu_rollout.py:1220-1238 layout)
-        if (mask_words || mask_bool) {
-            const int cs = cT.rotc[seat][cT.f2c[src]] * NONB;
-            uint64_t w[3] = {m0, m1, m2};
-            for (int q = 0; q < 3; ++q) {
-                uint64_t x = w[q];
-                while (x) {
-                    const int b = __builtin_ctzll(x) + 64 * q;
-                    x &= x - 1;
-                    const int bit = cs + cT.rotc[seat][b];
-                    atomicOr(&bits[bit >> 5], 1u << (bit & 31));
-                }
+    }
+    // canonical compact mask bits (gpu_rollout.py:1220-1238 layout): the two
+    // lanes of a piece take alternate destination bits
+    if (mov && (mask_words || mask_bool)) {
+        const int cs = rotl[flat_rank(cT.onm, src)] * NONB;
+        const uint64_t half = h ? 0xAAAAAAAAAAAAAAAAull : 0x5555555555555555ull;
+        uint64_t w[3] = {m0 & half, m1 & half, m2 & half};
+        for (int q = 0; q < 3; ++q) {
+            uint64_t x = w[q];
+            while (x) {
+                const int b = __builtin_ctzll(x) + 64 * q;
+                x &= x - 1;
+                const int bit = cs + rotl[b];
+                atomicOr(&bits[bit >> 5], 1u << (bit & 31));
             }
         }
     }

@@ -184,6 +184,39 @@ void build_tables(Tables &t)
                                  ((fl & CF_NG) ? 8 : 0) | ((fl & CF_ARC) ? 16 : 0));
         t.sh_other[f] = -1;
     }
+    // compact-cell forms
+    std::memset(t.adjc, 0xFF, sizeof t.adjc);
+    std::memset(t.raym, 0, sizeof t.raym);
+    std::memset(t.crayc, 0xFF, sizeof t.crayc);
+    std::memset(t.railidxc, -1, sizeof t.railidxc);
+    std::memset(t.campm, 0, sizeof t.campm);
+    for (int c = 0; c < NONB; ++c) {
+        const int f = t.c2f[c];
+        int n = 0;
+        for (int k = 0; k < 4; ++k) if (t.adj[f][k] >= 0) t.adjc[c][n++] = (uint8_t)t.f2c[t.adj[f][k]];
+        for (int k = 0; k < 4; ++k) if (t.diag[f][k] >= 0) t.adjc[c][n++] = (uint8_t)t.f2c[t.diag[f][k]];
+        if (flags(f) & CF_CAMP) t.campm[c >> 6] |= 1ull << (c & 63);
+        t.railidxc[c] = t.railidx[f];
+    }
+    std::memset(t.onm, 0, sizeof t.onm);
+    std::memset(t.railm, 0, sizeof t.railm);
+    std::memset(t.shm, 0, sizeof t.shm);
+    for (int f = 0; f < NC; ++f) {
+        const int fl = flags(f);
+        if (fl & CF_ON) t.onm[f >> 6] |= 1ull << (f & 63);
+        if (fl & CF_RAIL) t.railm[f >> 6] |= 1ull << (f & 63);
+        if (fl & CF_SH) t.shm[f >> 6] |= 1ull << (f & 63);
+    }
+    for (int i = 0; i < NRAIL; ++i) {
+        t.railc[i] = (uint8_t)t.f2c[t.railcell[i]];
+        for (int k = 0; k < 4; ++k)
+            for (int j = 0; j < t.raylen[i][k]; ++j) {
+                const int c = t.f2c[t.rays[i][k][j]];
+                t.raym[i][k][c >> 6] |= 1ull << (c & 63);
+            }
+        for (int d = 0; d < 2; ++d)
+            for (int j = 0; j < t.craylen[i][d]; ++j) t.crayc[i][d][j] = (uint8_t)t.f2c[t.crays[i][d][j]];
+    }
     for (int s = 0; s < 4; ++s) {
         int x1, y1, x2, y2;
         seat_cell(s, 26, x1, y1); seat_cell(s, 28, x2, y2);

@@ -43,6 +43,18 @@ struct Tables {
     int16_t sh_other[NC];         // stronghold cell -> the other stronghold of that seat
     int8_t owner[NC];             // owning seat or -1
     int8_t localidx[NC];          // slot index in the owner's rectangle or -1
+    // compact-cell forms for bitboard move generation (129-bit sets, bit c =
+    // compact cell c; compact order is flat order, so a straight run's cells
+    // rise (+x, +y) or fall (-x, -y) in compact index)
+    alignas(8) uint8_t adjc[NONB][8];     // road neighbours then camp diagonals, compact (0xFF none)
+    uint64_t raym[NRAIL][4][3];           // straight runs (+x, -x, +y, -y) as compact masks
+    alignas(16) uint8_t crayc[NRAIL][2][16];  // curve runs in walk order, compact (0xFF pad)
+    uint8_t railc[NRAIL];                 // rail index -> compact
+    int8_t railidxc[NONB];                // compact -> rail index or -1
+    uint64_t campm[3];                    // camp cells
+    // 289-bit flat masks: a cell's compact index is the number of on-board
+    // cells below it, its rail index the number of rail cells below it
+    uint64_t onm[5], railm[5], shm[5];
 };
 
 void build_tables(Tables &t);
