@@ -37,14 +37,39 @@ def test_version_and_errors(jl):
     assert b"bad field" in jl.lib.jq_last_error()
 
 
-_TABLES = np.dtype([
+def _struct(fields):
+    """numpy dtype of a C struct: fields (name, dtype, shape[, alignas]) laid out
+    with natural alignment, or the given alignas, like the compiler does."""
+    names, formats, offsets, off, maxal = [], [], [], 0, 1
+    for name, fmt, shape, *al in fields:
+        dt = np.dtype((fmt, shape))
+        align = al[0] if al else dt.base.alignment
+        off = (off + align - 1) // align * align
+        names.append(name); formats.append(dt); offsets.append(off)
+        off += dt.itemsize
+        maxal = max(maxal, align)
+    return np.dtype({"names": names, "formats": formats, "offsets": offsets,
+                     "itemsize": (off + maxal - 1) // maxal * maxal})
+
+
+# struct jq::Tables (junqi_amd/csrc/jq_topology.h)
+_TABLES = _struct([
     ("cflags", "<u2", (289,)), ("adj", "<i2", (289, 4)), ("diag", "<i2", (289, 4)), ("railidx", "i1", (289,)),
     ("railcell", "<i2", (73,)), ("rnbr", "<u8", (73, 2)), ("rays", "<i2", (73, 4, 12)), ("raylen", "i1", (73, 4)),
     ("crays", "<i2", (73, 2, 11)), ("craylen", "i1", (73, 2)), ("f2c", "<i2", (289,)), ("c2f", "<i2", (129,)),
     ("rot", "<i2", (4, 289)), ("unrot", "<i2", (4, 289)), ("rotc", "u1", (4, 129)), ("home", "<i2", (120,)),
     ("slotch", "i1", (30,)), ("statics", "u1", (289,)), ("sh_other", "<i2", (289,)), ("owner", "i1", (289,)),
     ("localidx", "i1", (289,)),
-], align=True)
+    ("adjc", "u1", (129, 8), 8), ("raym", "<u8", (73, 4, 3)), ("crayc", "u1", (73, 2, 16), 16),
+    ("railc", "u1", (73,)), ("railidxc", "i1", (129,)), ("campm", "<u8", (3,)), ("onm", "<u8", (5,)),
+    ("railm", "<u8", (5,)), ("shm", "<u8", (5,)),
+])
+
+
+def _bits(words, n):
+    """The first n bits of a little-endian uint64 word array, as a bool vector."""
+    w = np.asarray(words, np.uint64)
+    return ((w[np.arange(n) >> 6] >> (np.arange(n) & 63).astype(np.uint64)) & np.uint64(1)).astype(bool)
 
 
 def _product_tables(jl):
@@ -91,6 +116,47 @@ def test_board_tables_equal_oracle(jl):
         assert np.array_equal(t["unrot"][s][t["rot"][s]], np.arange(289))
     assert t["rot"][1][8 * 17 + 3] == 13 * 17 + 8    # WEST's centre camp (3,8) -> (8,13)
     assert t["rot"][3][8 * 17 + 13] == 13 * 17 + 8   # EAST's centre camp
+
+
+def test_compact_move_tables(jl):
+    """The compact-cell tables of the bitboard move generator against the oracle's
+    board (on-board / rail / stronghold / camp cells, compact order) and against
+    the flat run and neighbour tables they restate."""
+    t = _product_tables(jl)
+    o = O.tables()
+    c2f = o["compact_to_flat"].astype(np.int64)
+    f2c = np.full(289, -1, np.int64)
+    f2c[c2f] = np.arange(129)
+    assert np.array_equal(_bits(t["onm"], 289), o["on_board"] > 0)
+    assert np.array_equal(_bits(t["railm"], 289), o["rail"] > 0)
+    assert np.array_equal(_bits(t["shm"], 289), o["stronghold"] > 0)
+    assert np.array_equal(_bits(t["campm"], 129), o["camp"][c2f] > 0)
+    # ranks in the flat masks are the compact and rail indices
+    on, rail = o["on_board"] > 0, o["rail"] > 0
+    for f in range(289):
+        if on[f]:
+            assert int(on[:f].sum()) == f2c[f]
+        if rail[f]:
+            assert int(rail[:f].sum()) == t["railidx"][f] and t["railcell"][t["railidx"][f]] == f
+    assert np.array_equal(t["railc"], f2c[t["railcell"]])
+    assert np.array_equal(t["railidxc"], t["railidx"][c2f])
+    for c in range(129):
+        f = int(c2f[c])
+        want = {int(f2c[v]) for v in t["adj"][f] if v >= 0} | {int(f2c[v]) for v in t["diag"][f] if v >= 0}
+        got = [int(v) for v in t["adjc"][c] if v != 0xFF]
+        assert len(got) == len(set(got)) and set(got) == want, c
+    for i in range(73):
+        src = int(f2c[t["railcell"][i]])
+        for k in range(4):
+            cells = [int(f2c[v]) for v in t["rays"][i][k][: t["raylen"][i][k]]]
+            assert set(np.flatnonzero(_bits(t["raym"][i][k], 129))) == set(cells), (i, k)
+            # a straight run walks away from its source in compact order: up for +x / +y, down for -x / -y
+            seq = [src] + cells
+            assert all((b > a) if k in (0, 2) else (b < a) for a, b in zip(seq, seq[1:])), (i, k)
+        for d in range(2):
+            n = int(t["craylen"][i][d])
+            assert np.array_equal(t["crayc"][i][d][:n], f2c[t["crays"][i][d][:n]]), (i, d)
+            assert np.all(t["crayc"][i][d][n:] == 0xFF)
 
 
 @pytest.mark.parametrize("seed", [0, 1, 42, 2026, 123456789])
