@@ -1060,26 +1060,35 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
 }
 
 // Exclusive scan of counts into offsets (N+1); one 1024-thread block walks the
-// array in tiles of 4096: coalesced int4 loads (4 envs per thread), a wave scan
-// by shuffles, the 16 wave totals scanned through LDS, and a carry between tiles.
-constexpr int SCAN_THREADS = 1024, SCAN_TILE = 4 * SCAN_THREADS;
+// array in tiles of 32768 (one tile at the usual batch sizes): each thread
+// loads 32 consecutive counts with 16-byte loads, scans them in registers, the
+// 1024 thread totals are scanned by wave shuffles and the 16 wave totals
+// through LDS, and a carry runs between tiles.
+constexpr int SCAN_THREADS = 1024, SCAN_ITEMS = 32, SCAN_TILE = SCAN_THREADS * SCAN_ITEMS;
 __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                       int n)
 {
     __shared__ int32_t wsum[SCAN_THREADS / 64];
-    __shared__ int32_t carry_s;
+    __shared__ int32_t tile_total;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const bool vec = ((reinterpret_cast<uintptr_t>(counts) | reinterpret_cast<uintptr_t>(offsets)) & 15) == 0;
     int carry = 0;
     for (int base = 0; base < n; base += SCAN_TILE) {
-        const int i0 = base + 4 * t;
-        int v[4];
-        if (i0 + 3 < n && ((reinterpret_cast<uintptr_t>(counts + i0) & 15) == 0)) {
-            const int4 c = *reinterpret_cast<const int4 *>(counts + i0);
-            v[0] = c.x; v[1] = c.y; v[2] = c.z; v[3] = c.w;
+        const int i0 = base + SCAN_ITEMS * t;
+        int v[SCAN_ITEMS];
+        if (vec && i0 + SCAN_ITEMS <= n) {
+#pragma unroll
+            for (int k = 0; k < SCAN_ITEMS / 4; ++k) {
+                const int4 c = reinterpret_cast<const int4 *>(counts + i0)[k];
+                v[4 * k] = c.x; v[4 * k + 1] = c.y; v[4 * k + 2] = c.z; v[4 * k + 3] = c.w;
+            }
         } else {
-            for (int k = 0; k < 4; ++k) v[k] = i0 + k < n ? counts[i0 + k] : 0;
+#pragma unroll
+            for (int k = 0; k < SCAN_ITEMS; ++k) v[k] = i0 + k < n ? counts[i0 + k] : 0;
         }
-        const int tsum = v[0] + v[1] + v[2] + v[3];
+        int tsum = 0;
+#pragma unroll
+        for (int k = 0; k < SCAN_ITEMS; ++k) tsum += v[k];
         int incl = tsum;
         for (int o = 1; o < 64; o <<= 1) { const int u = __shfl_up(incl, o); if (lane >= o) incl += u; }
         if (lane == 63) wsum[w] = incl;
@@ -1089,46 +1098,86 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict
             int y = x;
             for (int o = 1; o < SCAN_THREADS / 64; o <<= 1) { const int u = __shfl_up(y, o); if (lane >= o) y += u; }
             if (lane < SCAN_THREADS / 64) wsum[lane] = y - x;   // exclusive wave prefix
-            if (lane == SCAN_THREADS / 64 - 1) carry_s = y;      // tile total
+            if (lane == SCAN_THREADS / 64 - 1) tile_total = y;
         }
         __syncthreads();
         int run = carry + wsum[w] + incl - tsum;
-        for (int k = 0; k < 4; ++k) {
-            if (i0 + k < n) offsets[i0 + k] = run;
-            run += v[k];
+        if (vec && i0 + SCAN_ITEMS <= n) {
+#pragma unroll
+            for (int k = 0; k < SCAN_ITEMS / 4; ++k) {
+                int4 o;
+                o.x = run; run += v[4 * k];
+                o.y = run; run += v[4 * k + 1];
+                o.z = run; run += v[4 * k + 2];
+                o.w = run; run += v[4 * k + 3];
+                reinterpret_cast<int4 *>(offsets + i0)[k] = o;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < SCAN_ITEMS; ++k) {
+                if (i0 + k < n) offsets[i0 + k] = run;
+                run += v[k];
+            }
         }
-        carry += carry_s;
+        carry += tile_total;
         __syncthreads();
     }
     if (t == 0) offsets[n] = carry;
 }
 
+// Position of the k-th set bit (k < popcount) of a 64-bit word.
+__device__ __forceinline__ int select64(uint64_t x, int k)
+{
+    int pos = 0;
+#pragma unroll
+    for (int width = 32; width >= 1; width >>= 1) {
+        const int c = __popcll(x & ((1ull << width) - 1ull));
+        if (k >= c) { k -= c; x >>= width; pos += width; }
+    }
+    return pos;
+}
+
 // Write each env's ids at its offset: pieces in ascending source order, each
-// piece's destinations ascending (compact order = flat order).
+// piece's destinations ascending (compact order = flat order). One wave per
+// env; lane j produces ids j, j + 64, ...: it finds its piece from the running
+// counts, the destination by selecting a bit of that piece's mask, and maps it
+// to a flat cell through an LDS copy of the compact table.
 __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict__ offsets, int32_t *__restrict__ values)
 {
     const int env = blockIdx.x, l = threadIdx.x;
     if (env >= S.n) return;
+    __shared__ int16_t c2f[NONB + 3];
+    __shared__ int32_t start[33];     // first id of each piece, start[n] = total
+    for (int c = l; c < NONB; c += 64) c2f[c] = cT.c2f[c];
     const LegalRec &G = S.lg[env];
     const int n = G.n;
     int cnt = 0, src = 0;
-    uint64_t m[3] = {0, 0, 0};
+    uint64_t m0 = 0, m1 = 0, m2 = 0;
     if (l < n) {
         src = G.src[l];
-        m[0] = G.mask[l][0]; m[1] = G.mask[l][1]; m[2] = G.mask[l][2];
-        cnt = __popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]);
+        m0 = G.mask[l][0]; m1 = G.mask[l][1]; m2 = G.mask[l][2];
+        cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
     }
     int incl = cnt;
     for (int o = 1; o < 64; o <<= 1) { const int v = __shfl_up(incl, o); if (l >= o) incl += v; }
-    int w = offsets[env] + incl - cnt;
-    if (l < n) {
-        for (int q = 0; q < 3; ++q) {
-            uint64_t x = m[q];
-            while (x) {
-                const int b = __builtin_ctzll(x) + 64 * q;
-                x &= x - 1;
-                values[w++] = src * NC + cT.c2f[b];
-            }
+    if (l < n) start[l] = incl - cnt;
+    const int total = __shfl(incl, 63);
+    if (l == 0) start[n] = total;
+    const int base = offsets[env];
+    __syncthreads();
+    for (int b = 0; b < total; b += 64) {   // uniform trip count: every lane takes the shuffles
+        const int i = b + l;
+        int j = 0;   // piece of id i: the last piece whose start is <= i
+        for (int step = 16; step >= 1; step >>= 1)
+            if (j + step < n && start[j + step] <= i) j += step;
+        const uint64_t w0 = __shfl(m0, j), w1 = __shfl(m1, j), w2 = __shfl(m2, j);
+        const int s = __shfl(src, j);
+        if (i < total) {
+            const int k = i - start[j];
+            const int c0 = __popcll(w0), c1 = __popcll(w1);
+            const int c = k < c0 ? select64(w0, k)
+                                 : k < c0 + c1 ? 64 + select64(w1, k - c0) : 128 + select64(w2, k - c0 - c1);
+            values[base + i] = s * NC + c2f[c];
         }
     }
 }
