@@ -628,7 +628,23 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     __shared__ int16_t pos[PID_STRIDE];
     __shared__ int8_t ptype[PID_STRIDE];
 
+    // the board, the piece records, the env record and the action are all
+    // loaded into registers first (one memory round trip), then staged in LDS;
+    // the checks below only decide whether the board is used
+    int8_t cv[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        const int f = l + 64 * k;
+        cv[k] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : (int8_t)-1;
+    }
+    const PieceRec r0 = S.piece[pc_idx(env, l)], r1 = S.piece[pc_idx(env, l + 64)];
+    const int32_t a = actions[env];
     const EnvRec &E = S.env[env];   // uniform: scalar loads
+#pragma unroll
+    for (int k = 0; k < 5; ++k)
+        if (l + 64 * k < CELL_STRIDE) cell[l + 64 * k] = cv[k];
+    pos[l] = r0.pos; ptype[l] = r0.ptype;
+    pos[l + 64] = r1.pos; ptype[l + 64] = r1.ptype;
     const bool was_term = E.term != 0;
     const int seat = E.turn;
     if (l == 0) {
@@ -644,7 +660,6 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     }
     if (was_term) return;
 
-    const int32_t a = actions[env];
     int src = -1, dst = -1;
     if (act_fmt == 1) {
         const int as = acting ? acting[env] : seat;
@@ -660,13 +675,6 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     if (acting && acting[env] != seat) return;
     const uint8_t sdead0 = E.sdead;
     if ((sdead0 >> seat) & 1) return;
-
-    for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
-    for (int p = l; p < PID_STRIDE; p += 64) {
-        const PieceRec r = S.piece[pc_idx(env, p)];
-        pos[p] = r.pos;
-        ptype[p] = r.ptype;
-    }
     __syncthreads();
     if (!legal_pair(cell, ptype, seat, src, dst)) return;
 
