@@ -196,6 +196,37 @@ int jq_finalize_import(jq_env *env, void *stream);
  * scalar fields such as the termination flags); beliefs are left as they are. */
 int jq_rehash(jq_env *env, void *stream);
 
+/* ---- compact rollout history ------------------------------------------------
+ * Pre-action state of every env at each of num_steps rollout steps (row
+ * step * num_envs + env), from which PPO minibatches are rebuilt: observations
+ * and canonical legal masks are recomputed for the requested rows instead of
+ * being stored. Every per-env block is kept (board, pieces, all four observers'
+ * combat memory and belief codes, remaining counts, counters, move ring):
+ * jq_history_bytes() = num_steps * num_envs * 35972 bytes. Replaces
+ * junqi_cuda.DeviceRolloutHistory (src/env/cuda/src/rollout_history.cu:160-525)
+ * behind GpuRolloutHistory (junqi_rl/gpu_rollout.py:107-217). */
+typedef struct jq_history jq_history;
+int jq_history_create(jq_history **out, int32_t num_envs, int32_t num_steps, int32_t show_mode, int32_t device);
+int jq_history_destroy(jq_history *hist);
+int jq_history_bytes(const jq_history *hist, int64_t *bytes);
+/* Copy env's current state into row block `step` (DeviceRolloutHistory::snapshot,
+ * rollout_history.cu:190-287). `acting` (device int8, N) is accepted for the
+ * reference's signature; all observers' beliefs are stored, so it is not read.
+ * env must have num_envs games, the history's show mode and device. */
+int jq_history_snapshot(jq_history *hist, jq_env *env, const int8_t *acting, int32_t step, void *stream);
+/* Rebuild `batch` rows: flat (device int64, batch) row indices, observer (device
+ * int8, batch) the seat each row is observed and masked for. Writes spatial /
+ * aux / global like jq_observe (fmt JQ_OBS_*), and the canonical legal mask of
+ * the observer seat as mask_words (device int32 (batch, 521)) and/or mask_bool
+ * (device uint8 (batch, 16641)); any output may be NULL. Rows outside
+ * [0, num_steps * num_envs) are rebuilt from the empty terminated state.
+ * (DeviceRolloutHistory::reconstruct, rollout_history.cu:289-523.) Internal
+ * scratch of `batch` rows is kept between calls (grown when needed), so calls
+ * on one history must not overlap on different streams. */
+int jq_history_reconstruct(jq_history *hist, const int64_t *flat, const int8_t *observer, int32_t batch, int32_t fmt,
+                           void *spatial, float *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
+                           void *stream);
+
 /* Synchronise `stream`. */
 int jq_sync(void *stream);
 

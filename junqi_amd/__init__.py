@@ -11,6 +11,7 @@ from ._lib import AUX_CHANNELS, JunqiError
 from .batch import JunqiBatch, decode_table, generate_lineups, generate_pool, recency_table, zobrist_stream
 from .gpu_rollout import GpuRollout
 from .gpu_world import GpuWorld
+from .history import GpuRolloutHistory
 
-__all__ = ["JunqiBatch", "GpuRollout", "GpuWorld", "JunqiError", "AUX_CHANNELS", "decode_table",
+__all__ = ["JunqiBatch", "GpuRollout", "GpuWorld", "GpuRolloutHistory", "JunqiError", "AUX_CHANNELS", "decode_table",
            "generate_lineups", "generate_pool", "recency_table", "zobrist_stream", "_lib"]

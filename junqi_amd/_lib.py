@@ -40,7 +40,8 @@ _EXPORTS = [
     "jq_generate_lineups", "jq_generate_pool", "jq_board_tables", "jq_reset_terminated", "jq_step",
     "jq_legal", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_env_step",
     "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import", "jq_rehash",
-    "jq_sync",
+    "jq_sync", "jq_history_create", "jq_history_destroy", "jq_history_bytes", "jq_history_snapshot",
+    "jq_history_reconstruct",
 ]
 
 
@@ -79,6 +80,10 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_field_ptr": ([P, I32, C.POINTER(P), C.POINTER(I64), C.POINTER(I64)], C.c_int),
         "jq_finalize_import": ([P, P], C.c_int), "jq_rehash": ([P, P], C.c_int),
         "jq_sync": ([P], C.c_int),
+        "jq_history_create": ([C.POINTER(P), I32, I32, I32, I32], C.c_int),
+        "jq_history_destroy": ([P], C.c_int), "jq_history_bytes": ([P, C.POINTER(I64)], C.c_int),
+        "jq_history_snapshot": ([P, P, P, I32, P], C.c_int),
+        "jq_history_reconstruct": ([P, P, P, I32, I32, P, P, P, P, P, P], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

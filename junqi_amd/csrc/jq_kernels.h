@@ -790,23 +790,27 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
 }
 
 // ------------------------------------------------------------------ reset
-// Empty, terminated state for every env (before the first reset).
-__global__ __launch_bounds__(64) void k_clear(State S)
+// Empty, terminated state of one env (no pieces, empty board, zero beliefs),
+// written by threads t of nt.
+__device__ __forceinline__ void clear_env(const State &S, int env, int t, int nt)
 {
-    const int env = blockIdx.x, l = threadIdx.x;
-    if (env >= S.n) return;
-    for (int f = l; f < CELL_STRIDE; f += 64) S.cell[(size_t)env * CELL_STRIDE + f] = -1;
+    for (int f = t; f < CELL_STRIDE; f += nt) S.cell[(size_t)env * CELL_STRIDE + f] = -1;
     PieceRec r;
     r.pos = r.zero = r.dstep = r.dloc = -1;
     r.mcount = r.aeat = r.psurv = 0;
     r.ptype = r.dreason = -1;
     CmRec c = {};
     c.ldir = c.lchain = c.fstep = -1;
-    for (int p = l; p < PID_STRIDE; p += 64) {
+    for (int p = t; p < PID_STRIDE; p += nt) {
         S.piece[pc_idx(env, p)] = r;
-        for (int o = 0; o < 4; ++o) S.cm[cm_idx(env, o, p)] = c;
+        for (int o = 0; o < 4; ++o) {
+            S.cm[cm_idx(env, o, p)] = c;
+            S.bcode[((size_t)env * 4 + o) * PID_STRIDE + p] = 0;
+        }
     }
-    if (l == 0) {
+    for (int k = t; k < 4 * 48; k += nt) S.rem[(size_t)env * 4 * 48 + k] = 0;
+    for (int k = t; k < HIST_LEN; k += nt) S.hist[(size_t)env * HIST_LEN + k] = 0;
+    if (t == 0) {
         EnvRec E = {};
         E.winner = -1;
         E.term = 1;
@@ -814,6 +818,14 @@ __global__ __launch_bounds__(64) void k_clear(State S)
         S.lg[env].n = 0;
         S.lg[env].seat = 0;
     }
+}
+
+// Empty, terminated state for every env (before the first reset).
+__global__ __launch_bounds__(64) void k_clear(State S)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    clear_env(S, env, l, 64);
 }
 
 // Start an env from a lineup (GameState.new_game, state.py:490-620; beliefs,

@@ -16,6 +16,7 @@
 #include "jq_device.h"
 #include "jq_kernels.h"
 #include "jq_obs.h"
+#include "jq_history.h"
 #include "jq_topology.h"
 
 using namespace jq;
@@ -27,6 +28,18 @@ struct jq_env {
     bool zob_ready = false, rlut_ready = false;
     int32_t *tmp_actions = nullptr;
     int obs_blocks = 0;              // resident u8 observation blocks on the device
+};
+
+// Rollout history: per-step copies of every per-env state block.
+struct jq_history {
+    int device = 0;
+    int32_t show_mode = 0, max_moves = 0;
+    HistState H{};
+    std::vector<void *> allocs;
+    float *rlut = nullptr;           // recency table copied from the snapshotted handle
+    bool rlut_ready = false;
+    jq_env *replay = nullptr;        // scratch state of the rebuilt rows
+    int32_t replay_cap = 0;
 };
 
 namespace {
@@ -123,6 +136,18 @@ int dalloc(jq_env *e, T *&p, size_t count, int fill_byte)
     if (hipMalloc(&q, bytes) != hipSuccess) return fail(JQ_E_OOM, "hipMalloc(%zu) failed", bytes);
     e->allocs.push_back(q);
     if (hipMemset(q, fill_byte, bytes) != hipSuccess) return fail(JQ_E_HIP, "hipMemset failed");
+    p = static_cast<T *>(q);
+    return JQ_OK;
+}
+
+template <class T>
+int halloc(jq_history *h, T *&p, size_t count)
+{
+    void *q = nullptr;
+    const size_t bytes = count * sizeof(T);
+    if (hipMalloc(&q, bytes) != hipSuccess) return fail(JQ_E_OOM, "hipMalloc(%zu) failed", bytes);
+    h->allocs.push_back(q);
+    if (hipMemset(q, 0, bytes) != hipSuccess) return fail(JQ_E_HIP, "hipMemset failed");
     p = static_cast<T *>(q);
     return JQ_OK;
 }
@@ -519,6 +544,116 @@ int jq_rehash(jq_env *e, void *stream)
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables first");
     hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 0);
     return launch_check("k_finalize");
+}
+
+// ---------------------------------------------------------------- history
+int jq_history_create(jq_history **out, int32_t num_envs, int32_t num_steps, int32_t show_mode, int32_t device)
+{
+    if (!out) return fail(JQ_E_ARG, "out is null");
+    *out = nullptr;
+    if (num_envs <= 0 || num_envs > (1 << 24)) return fail(JQ_E_ARG, "num_envs %d out of range", num_envs);
+    if (num_steps <= 0) return fail(JQ_E_ARG, "num_steps must be positive, got %d", num_steps);
+    if ((int64_t)num_envs * num_steps > ((int64_t)1 << 31)) return fail(JQ_E_ARG, "num_steps * num_envs too large");
+    if (show_mode < 0 || show_mode > 2) return fail(JQ_E_ARG, "show_mode %d not in {0,1,2}", show_mode);
+    int ndev = 0;
+    HIP_TRY(hipGetDeviceCount(&ndev));
+    if (device < 0 || device >= ndev) return fail(JQ_E_ARG, "device %d not present (%d devices)", device, ndev);
+    HIP_TRY(hipSetDevice(device));
+    jq_history *h = new jq_history();
+    h->device = device;
+    h->show_mode = show_mode;
+    HistState &H = h->H;
+    H.steps = num_steps; H.n = num_envs;
+    const size_t R = (size_t)num_steps * num_envs;
+    int rc;
+#define A(ptr, cnt) do { if ((rc = halloc(h, ptr, cnt)) != 0) { jq_history_destroy(h); return rc; } } while (0)
+    A(H.cell, R * CELL_STRIDE);
+    A(H.piece, R * PID_STRIDE);
+    A(H.cm, R * 4 * PID_STRIDE);
+    A(H.bcode, R * 4 * PID_STRIDE);
+    A(H.rem, R * 4 * 48);
+    A(H.env, R);
+    A(H.hist, R * HIST_LEN);
+    A(h->rlut, 4 * 4096);
+#undef A
+    *out = h;
+    return JQ_OK;
+}
+
+int jq_history_destroy(jq_history *h)
+{
+    if (!h) return JQ_OK;
+    (void)hipSetDevice(h->device);
+    if (h->replay) jq_destroy(h->replay);
+    for (void *p : h->allocs) (void)hipFree(p);
+    delete h;
+    return JQ_OK;
+}
+
+int jq_history_bytes(const jq_history *h, int64_t *bytes)
+{
+    if (!h || !bytes) return fail(JQ_E_ARG, "null argument");
+    *bytes = (int64_t)h->H.steps * h->H.n * (int64_t)HIST_ROW_BYTES;
+    return JQ_OK;
+}
+
+int jq_history_snapshot(jq_history *h, jq_env *e, const int8_t *acting, int32_t step, void *stream)
+{
+    (void)acting;
+    if (!h || !e) return fail(JQ_E_ARG, "null handle");
+    const HistState &H = h->H;
+    if (e->S.n != H.n) return fail(JQ_E_ARG, "history/state num_envs mismatch (%d vs %d)", H.n, e->S.n);
+    if (e->device != h->device) return fail(JQ_E_ARG, "history and state live on different devices");
+    if (e->S.show_mode != h->show_mode) return fail(JQ_E_ARG, "history and state show modes differ");
+    if (step < 0 || step >= H.steps) return fail(JQ_E_ARG, "history snapshot step %d out of range [0, %d)", step, H.steps);
+    if (!e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded to the state handle");
+    HIP_TRY(hipSetDevice(h->device));
+    hipStream_t s = strm(stream);
+    const size_t n = (size_t)H.n, r0 = (size_t)step * n;
+    const State &S = e->S;
+    HIP_TRY(hipMemcpyAsync(H.cell + r0 * CELL_STRIDE, S.cell, n * CELL_STRIDE, hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(H.piece + r0 * PID_STRIDE, S.piece, n * PID_STRIDE * sizeof(PieceRec), hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(H.cm + r0 * 4 * PID_STRIDE, S.cm, n * 4 * PID_STRIDE * sizeof(CmRec), hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(H.bcode + r0 * 4 * PID_STRIDE, S.bcode, n * 4 * PID_STRIDE, hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(H.rem + r0 * 4 * 48, S.rem, n * 4 * 48, hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(H.env + r0, S.env, n * sizeof(EnvRec), hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(H.hist + r0 * HIST_LEN, S.hist, n * HIST_LEN * sizeof(int32_t), hipMemcpyDeviceToDevice, s));
+    if (!h->rlut_ready) {
+        HIP_TRY(hipMemcpyAsync(h->rlut, S.rlut, 4 * 4096 * sizeof(float), hipMemcpyDeviceToDevice, s));
+        h->rlut_ready = true;
+    }
+    h->max_moves = S.max_moves;
+    return JQ_OK;
+}
+
+int jq_history_reconstruct(jq_history *h, const int64_t *flat, const int8_t *observer, int32_t batch, int32_t fmt,
+                           void *spatial, float *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
+                           void *stream)
+{
+    if (!h) return fail(JQ_E_ARG, "null history");
+    if (batch <= 0) return fail(JQ_E_ARG, "cannot reconstruct an empty history minibatch");
+    if (!flat || !observer) return fail(JQ_E_ARG, "history reconstruction received a null device pointer");
+    if (!h->rlut_ready) return fail(JQ_E_STATE, "history has no snapshot yet");
+    HIP_TRY(hipSetDevice(h->device));
+    int rc;
+    if (h->replay_cap < batch) {   // scratch rows, grown to the largest batch seen
+        if (h->replay) { jq_destroy(h->replay); h->replay = nullptr; h->replay_cap = 0; }
+        if ((rc = jq_create(&h->replay, batch, std::max(1, h->max_moves), h->show_mode, h->device)) != 0) return rc;
+        h->replay_cap = batch;
+    }
+    jq_env *R = h->replay;
+    R->S.n = batch;
+    R->S.rlut = h->rlut;
+    R->rlut_ready = true;
+    hipLaunchKernelGGL(k_history_gather, dim3(batch), dim3(256), 0, strm(stream), h->H, flat, batch, R->S);
+    if ((rc = launch_check("k_history_gather")) != 0) return rc;
+    if (spatial || aux || global) {
+        if (!spatial || !global) return fail(JQ_E_ARG, "spatial and global outputs go together");
+        if ((rc = jq_observe(R, observer, fmt, 0, spatial, aux, global, stream)) != 0) return rc;
+    }
+    if (mask_words || mask_bool)
+        if ((rc = jq_legal(R, observer, nullptr, nullptr, nullptr, mask_words, mask_bool, stream)) != 0) return rc;
+    return JQ_OK;
 }
 
 int jq_sync(void *stream)

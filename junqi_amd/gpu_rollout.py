@@ -19,6 +19,7 @@ import torch
 
 from . import _lib as L
 from .batch import JunqiBatch, generate_pool
+from .history import GpuRolloutHistory
 
 DEFAULT_POOL_SIZE = 10000
 OBS_CHANNELS = L.OBS_CHANNELS
@@ -240,8 +241,16 @@ class GpuRollout:
     def draw_torch(self) -> torch.Tensor:
         return self._b.field_tensor("draw", torch.bool)
 
-    def create_rollout_history(self, num_steps: int):
-        raise NotImplementedError("rollout-history compaction (rollout_history.cu) is not part of this build")
+    @property
+    def state(self) -> JunqiBatch:
+        """The device game-state batch (the reference's DeviceGameStateBatch)."""
+        return self._b
+
+    def create_rollout_history(self, num_steps: int) -> GpuRolloutHistory:
+        """Allocate compact pre-action state history for one PPO rollout
+        (gpu_rollout.py:579-585)."""
+        return GpuRolloutHistory(num_steps=num_steps, num_envs=self.num_envs, show_mode=self.show_mode,
+                                 device_id=self._device_id)
 
     def close(self) -> None:
         self._b.close()
