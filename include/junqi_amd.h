@@ -227,6 +227,23 @@ int jq_history_reconstruct(jq_history *hist, const int64_t *flat, const int8_t *
                            void *spatial, float *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
                            void *stream);
 
+/* ---- legal-support storage: dense mask rows <-> id lists ----------------------
+ * Rollout buffers keep each transition's legal support as ids
+ * (junqi_rl/training/rollout_gpu.py:119-198). jq_mask_count: counts (device
+ * int32, n) = nonzero bytes of each row of a dense (n, d) uint8 mask.
+ * jq_mask_to_ids: ids (device int32, (n, k_max)) = each row's nonzero columns in
+ * order, then zeros; every count must be <= k_max (check jq_mask_count first:
+ * _dense_mask_to_csr raises before it writes, rollout_gpu.py:119-167).
+ * jq_ids_to_mask: out (device uint8, (batch, d)) = rows idx (device int64,
+ * batch) of the (rows, k_max) id lists with their counts as dense rows; ids
+ * outside [0, d) and rows outside [0, rows) leave zeros
+ * (_csr_to_dense_selected, rollout_gpu.py:170-198). Launched on the current
+ * device. */
+int jq_mask_count(const uint8_t *mask, int32_t n, int32_t d, int32_t *counts, void *stream);
+int jq_mask_to_ids(const uint8_t *mask, int32_t n, int32_t d, int32_t k_max, int32_t *ids, void *stream);
+int jq_ids_to_mask(const int32_t *ids, const int32_t *counts, int64_t rows, int32_t k_max, const int64_t *idx,
+                   int32_t batch, int32_t d, uint8_t *out, void *stream);
+
 /* Synchronise `stream`. */
 int jq_sync(void *stream);
 

@@ -17,6 +17,7 @@
 #include "jq_kernels.h"
 #include "jq_obs.h"
 #include "jq_history.h"
+#include "jq_masks.h"
 #include "jq_topology.h"
 
 using namespace jq;
@@ -654,6 +655,37 @@ int jq_history_reconstruct(jq_history *h, const int64_t *flat, const int8_t *obs
     if (mask_words || mask_bool)
         if ((rc = jq_legal(R, observer, nullptr, nullptr, nullptr, mask_words, mask_bool, stream)) != 0) return rc;
     return JQ_OK;
+}
+
+// ---------------------------------------------------------------- masks
+int jq_mask_count(const uint8_t *mask, int32_t n, int32_t d, int32_t *counts, void *stream)
+{
+    if (!mask || !counts) return fail(JQ_E_ARG, "null device pointer");
+    if (n < 0 || d <= 0) return fail(JQ_E_ARG, "bad mask shape (%d, %d)", n, d);
+    if (n == 0) return JQ_OK;
+    hipLaunchKernelGGL(k_mask_count, dim3(n), dim3(64), 0, strm(stream), mask, n, d, counts);
+    return launch_check("k_mask_count");
+}
+
+int jq_mask_to_ids(const uint8_t *mask, int32_t n, int32_t d, int32_t k_max, int32_t *ids, void *stream)
+{
+    if (!mask || !ids) return fail(JQ_E_ARG, "null device pointer");
+    if (n < 0 || d <= 0 || k_max <= 0) return fail(JQ_E_ARG, "bad shapes (n %d, d %d, k_max %d)", n, d, k_max);
+    if (n == 0) return JQ_OK;
+    hipLaunchKernelGGL(k_mask_to_ids, dim3(n), dim3(64), 0, strm(stream), mask, n, d, k_max, ids);
+    return launch_check("k_mask_to_ids");
+}
+
+int jq_ids_to_mask(const int32_t *ids, const int32_t *counts, int64_t rows, int32_t k_max, const int64_t *idx,
+                   int32_t batch, int32_t d, uint8_t *out, void *stream)
+{
+    if (!ids || !counts || !idx || !out) return fail(JQ_E_ARG, "null device pointer");
+    if (rows < 0 || k_max <= 0 || batch < 0 || d <= 0)
+        return fail(JQ_E_ARG, "bad shapes (rows %lld, k_max %d, batch %d, d %d)", (long long)rows, k_max, batch, d);
+    if (batch == 0) return JQ_OK;
+    hipLaunchKernelGGL(k_ids_to_mask, dim3(batch), dim3(256), 0, strm(stream), ids, counts, rows, k_max, idx, batch, d,
+                       out);
+    return launch_check("k_ids_to_mask");
 }
 
 int jq_sync(void *stream)

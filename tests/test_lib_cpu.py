@@ -218,3 +218,24 @@ def test_mirror_helpers_without_gpu():
     assert sd["alive"].shape == (240,) and sd["cell_piece_id"].shape == (578,) and sd["seat_dead_arr"].shape == (8,)
     assert sd["turn"].tolist() == [2, 2] and sd["move_counter"].tolist() == [7, 7]
     assert extra["winner_team"].tolist() == [-1, -1] and extra["move_history"] == [[(10, 27)], [(10, 27)]]
+
+
+def test_mask_helpers_validate_without_gpu():
+    """Argument checks of the legal-support helpers that need no device; the
+    helpers refuse host tensors instead of falling back to a host path."""
+    import torch
+
+    from junqi_amd.masks import csr_to_dense_selected, dense_mask_to_csr
+
+    m = torch.zeros((4, 16641), dtype=torch.bool)
+    with pytest.raises(ValueError, match="2-D bool"):
+        dense_mask_to_csr(m.to(torch.uint8), torch.zeros((4, 8), dtype=torch.int32), torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="shapes"):
+        dense_mask_to_csr(m, torch.zeros((4, 0), dtype=torch.int32), torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="int32"):
+        dense_mask_to_csr(m, torch.zeros((4, 8), dtype=torch.int64), torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="CUDA"):
+        dense_mask_to_csr(m, torch.zeros((4, 8), dtype=torch.int32), torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="CUDA"):
+        csr_to_dense_selected(torch.zeros((4, 8), dtype=torch.int32), torch.zeros(4, dtype=torch.int32),
+                              torch.zeros(2, dtype=torch.int64), 16641)
