@@ -127,6 +127,18 @@ int jq_legal(jq_env *env, const int8_t *acting, int32_t *counts, int32_t *offset
 int jq_observe(jq_env *env, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial,
                float *aux, float *global, void *stream);
 
+/* Uploaded beliefs: copy (N, 4, 12, 289) float32 world-cell beliefs per (env,
+ * observer) into the handle (from host memory if from_host, else from device
+ * memory; the buffer is allocated on the first call) and make jq_observe read
+ * its belief planes 12-23 and 27-50 from them: the observer's value at each
+ * teammate / enemy piece's cell where > 0 (upload_beliefs,
+ * junqi_rl/gpu_rollout.py:966-981; observation.cu:246-372). Globals keep the
+ * BeliefTensor remaining counts. Such observations are JQ_OBS_F32 / JQ_OBS_BF16
+ * only (arbitrary floats have no u8 code). jq_clear_beliefs returns to the
+ * handle's own BeliefTensor beliefs. */
+int jq_upload_beliefs(jq_env *env, const void *beliefs, int32_t from_host, void *stream);
+int jq_clear_beliefs(jq_env *env);
+
 /* The 256-entry float32 decode table of JQ_OBS_U8 codes (host pointer out). */
 int jq_obs_decode_table(float *host_out256);
 

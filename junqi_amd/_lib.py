@@ -41,7 +41,8 @@ _EXPORTS = [
     "jq_legal", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_env_step",
     "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import", "jq_rehash",
     "jq_sync", "jq_history_create", "jq_history_destroy", "jq_history_bytes", "jq_history_snapshot",
-    "jq_history_reconstruct", "jq_mask_count", "jq_mask_to_ids", "jq_ids_to_mask",
+    "jq_history_reconstruct", "jq_mask_count", "jq_mask_to_ids", "jq_ids_to_mask", "jq_upload_beliefs",
+    "jq_clear_beliefs",
 ]
 
 
@@ -86,6 +87,7 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_history_reconstruct": ([P, P, P, I32, I32, P, P, P, P, P, P], C.c_int),
         "jq_mask_count": ([P, I32, I32, P, P], C.c_int), "jq_mask_to_ids": ([P, I32, I32, I32, P, P], C.c_int),
         "jq_ids_to_mask": ([P, P, I64, I32, P, I32, I32, P, P], C.c_int),
+        "jq_upload_beliefs": ([P, P, I32, P], C.c_int), "jq_clear_beliefs": ([P], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -224,6 +224,30 @@ class JunqiBatch:
             return out_spatial, out_global, out_aux
         return out_spatial, out_global
 
+    def upload_beliefs(self, beliefs) -> None:
+        """Observations read their belief planes from (N, 4, 12, 289) float32
+        world-cell beliefs (host array or device tensor) until clear_beliefs()."""
+        shape = (self.n, 4, 12, 289)
+        if isinstance(beliefs, torch.Tensor):
+            if tuple(beliefs.shape) != shape:
+                raise ValueError(f"beliefs shape must be {shape}, got {tuple(beliefs.shape)}")
+            if beliefs.device.type != "cuda":
+                beliefs = beliefs.numpy()
+            else:
+                src = beliefs.to(device=self.device, dtype=torch.float32).contiguous()
+                self._bel_src = src   # kept alive until the copy has run
+                check(lib.jq_upload_beliefs(self._h, src.data_ptr(), 0, self.stream))
+                return
+        a = np.ascontiguousarray(beliefs, dtype=np.float32)
+        if a.shape != shape:
+            raise ValueError(f"beliefs shape must be {shape}, got {a.shape}")
+        check(lib.jq_upload_beliefs(self._h, a.ctypes.data, 1, self.stream))
+        torch.cuda.synchronize(self.device)   # the host array may go away
+
+    def clear_beliefs(self) -> None:
+        """Return observations to the device's own BeliefTensor beliefs."""
+        check(lib.jq_clear_beliefs(self._h))
+
     # ------------------------------------------------------------ sampling / fused step
     def sample_uniform(self, seed: int, ply: int, out: torch.Tensor | None = None) -> torch.Tensor:
         if out is None:

@@ -29,6 +29,8 @@ struct jq_env {
     bool zob_ready = false, rlut_ready = false;
     int32_t *tmp_actions = nullptr;
     int obs_blocks = 0;              // resident u8 observation blocks on the device
+    float *ext_bel = nullptr;        // uploaded (N, 4, 12, 289) beliefs, allocated on first upload
+    bool ext_on = false;             // observations read the uploaded beliefs
 };
 
 // Rollout history: per-step copies of every per-env state block.
@@ -413,9 +415,22 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
     if ((fmt != JQ_OBS_U8 || aux) && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
     const int nrows = all_seats ? e->S.n * 4 : e->S.n;
     const dim3 grid(nrows), block(OBS_THREADS);
+    if (e->ext_on && fmt == JQ_OBS_U8)
+        return fail(JQ_E_STATE, "uploaded beliefs are arbitrary floats: observe them as JQ_OBS_F32 or JQ_OBS_BF16");
+    const float *x = e->ext_bel;
     switch (fmt) {
-    case JQ_OBS_F32: hipLaunchKernelGGL(k_observe<0>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
-    case JQ_OBS_BF16: hipLaunchKernelGGL(k_observe<1>, grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows); break;
+    case JQ_OBS_F32:
+        if (e->ext_on)
+            hipLaunchKernelGGL((k_observe<0, true>), grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, x);
+        else
+            hipLaunchKernelGGL((k_observe<0, false>), grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, nullptr);
+        break;
+    case JQ_OBS_BF16:
+        if (e->ext_on)
+            hipLaunchKernelGGL((k_observe<1, true>), grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, x);
+        else
+            hipLaunchKernelGGL((k_observe<1, false>), grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, nullptr);
+        break;
     default:
         if ((rc = obs_u8_grid(e)) != 0) return rc;
         hipLaunchKernelGGL(k_observe_u8_persist, dim3(std::min(nrows, e->obs_blocks)), dim3(OBS_THREADS), 0,
@@ -424,6 +439,32 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
         break;
     }
     return launch_check("k_observe");
+}
+
+int jq_upload_beliefs(jq_env *e, const void *beliefs, int32_t from_host, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!beliefs) return fail(JQ_E_ARG, "null beliefs");
+    const size_t bytes = (size_t)e->S.n * 4 * 12 * NC * sizeof(float);
+    if (!e->ext_bel) {
+        void *q = nullptr;
+        if (hipMalloc(&q, bytes) != hipSuccess) return fail(JQ_E_OOM, "hipMalloc(%zu) for uploaded beliefs failed", bytes);
+        e->allocs.push_back(q);
+        e->ext_bel = static_cast<float *>(q);
+    }
+    HIP_TRY(hipMemcpyAsync(e->ext_bel, beliefs, bytes, from_host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
+                           strm(stream)));
+    e->ext_on = true;
+    return JQ_OK;
+}
+
+int jq_clear_beliefs(jq_env *e)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    e->ext_on = false;
+    return JQ_OK;
 }
 
 int jq_obs_decode_table(float *out)

@@ -76,6 +76,14 @@ struct ObsLds {
     float turnv[2];
 };
 
+// Uploaded beliefs (f32 / bf16 only): the 12 values of each teammate / enemy
+// piece, read at its world cell from the observer's (12, 289) slice, and the
+// piece's relation (1 teammate, 2 left, 3 right, 0 none).
+struct ExtLds {
+    float bel[PID_STRIDE][12];
+    uint8_t rel[PID_STRIDE];
+};
+
 // Byte-image address of element e of the range starting at `start` (image base
 // `base`) for a row whose first element sits at element phase m (row address /
 // element size, mod 16 / element size).
@@ -175,8 +183,10 @@ __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int
 }
 
 // Scatter one pid's nonzero elements into bits / img.
+template <bool EXT = false>
 __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, int m, const PieceIn &P,
-                                              const float rc[4], const uint32_t own_types[4], ObsLds &L)
+                                              const float rc[4], const uint32_t own_types[4], ObsLds &L,
+                                              const float *ext = nullptr, ExtLds *X = nullptr)
 {
     const int tm = (obs + 2) & 3, le = (obs + 1) & 3, team = obs & 1;
     const int s = pid / 30;
@@ -192,7 +202,13 @@ __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, i
         if (rel == 3) set_el(L, 26 * NC + k);
         if (rel == 1 && show_mode == SM_DARK) set_el(L, 24 * NC + k);
         // beliefs (12-23 teammate, 27-38 left, 39-50 right)
-        if (rel != 0) {
+        if (EXT && rel != 0) {   // uploaded: kept as floats, emitted per element
+            for (int j = 0; j < 12; ++j) {
+                const float v = ext[j * NC + P.pos];
+                X->bel[pid][j] = v > 0.f ? v : 0.f;
+            }
+            X->rel[pid] = (uint8_t)rel;
+        } else if (rel != 0) {
             const int bc = P.bcode < BC_COUNT ? P.bcode : 0;
             const int c0 = rel == 1 ? 12 : rel == 2 ? 27 : 39;
             const int base = rel == 1 ? RG0_B : RG1_B, start = rel == 1 ? RG0_S : RG1_S;
@@ -394,8 +410,9 @@ __device__ __forceinline__ void row_fetch(const State &S, int env, int obs, int 
 // Fill a cleared buffer with row (env, obs) from the fetched inputs, thread t
 // in [0, 256). Only the recency-table gathers are loads here. No thread reads
 // what another one writes, so no barrier is needed inside.
+template <bool EXT = false>
 __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, const RowIn &R, ObsLds &L,
-                                         float *glob_row)
+                                         float *glob_row, const float *ext = nullptr, ExtLds *X = nullptr)
 {
     const int pid = t < PID_STRIDE ? piece_of_thread(t, obs) : -1;
     if (pid >= 0) {
@@ -406,7 +423,7 @@ __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, 
             rc[2] = recency_at(S, R.mc, R.P.lchain, 2);
             rc[3] = recency_at(S, R.mc, R.P.fstep, 3);
         }
-        piece_scatter(S.show_mode, obs, pid, m, R.P, rc, R.own_types, L);
+        piece_scatter<EXT>(S.show_mode, obs, pid, m, R.P, rc, R.own_types, L, ext, X);
     } else if (t < PID_STRIDE) {   // the 8 spare threads clear the padding pids' recency
         const int pad = NP + (t < 64 ? t - 60 : t - 120);
         for (int q = 0; q < 4; ++q) L.rec[pad][q] = 0.f;
@@ -466,10 +483,28 @@ __device__ __forceinline__ float obs_cont_at(const ObsLds &L, int c, int k)
     return pid >= 0 ? L.rec[pid][c - 253] : 0.f;
 }
 
-// Value bits of element e in format FMT (0 f32, 1 bf16, 2 u8 code).
-template <int FMT>
-__device__ __forceinline__ uint32_t obs_elem(const ObsLds &L, int e, int m)
+// Belief planes written per element when beliefs are uploaded: 12-23, 27-50.
+constexpr int EB0_S = 12 * NC, EB0_E = 24 * NC, EB1_S = 27 * NC, EB1_E = 51 * NC;
+
+// Uploaded belief of plane c (12..23 teammate, 27..38 left, 39..50 right) at cell k.
+__device__ __forceinline__ float ext_belief_at(const ObsLds &L, const ExtLds *X, int c, int k)
 {
+    const int pid = L.cpid[k];
+    if (pid < 0) return 0.f;
+    const int want = c < 24 ? 1 : c < 39 ? 2 : 3;
+    const int j = c < 24 ? c - 12 : c < 39 ? c - 27 : c - 39;
+    return X->rel[pid] == want ? X->bel[pid][j] : 0.f;
+}
+
+// Value bits of element e in format FMT (0 f32, 1 bf16, 2 u8 code).
+template <int FMT, bool EXT = false>
+__device__ __forceinline__ uint32_t obs_elem(const ObsLds &L, int e, int m, const ExtLds *X = nullptr)
+{
+    if (EXT && ((e >= EB0_S && e < EB0_E) || (e >= EB1_S && e < EB1_E))) {
+        const int c = e / NC;
+        const float v = ext_belief_at(L, X, c, e - c * NC);
+        return FMT == 0 ? __float_as_uint(v) : (uint32_t)f32_to_bf16_rne(v);
+    }
     if (FMT != 2 && ((e >= CT0_S && e < CT0_E) || (e >= CT1_S && e < CT1_E))) {
         const int c = e / NC;
         const float v = obs_cont_at(L, c, e - c * NC);
@@ -529,11 +564,12 @@ __device__ __forceinline__ uint4 obs_chunk(const ObsLds &L, int e0, int off, boo
 }
 
 // Elements [e, f) of the row written one by one (row ends, continuous planes).
-template <int FMT>
-__device__ __forceinline__ void obs_elems(const ObsLds &L, uint8_t *row, int e, int f, int m)
+template <int FMT, bool EXT = false>
+__device__ __forceinline__ void obs_elems(const ObsLds &L, uint8_t *row, int e, int f, int m,
+                                          const ExtLds *X = nullptr)
 {
     for (; e < f; ++e) {
-        const uint32_t v = obs_elem<FMT>(L, e, m);
+        const uint32_t v = obs_elem<FMT, EXT>(L, e, m, X);
         if (FMT == 2) row[e] = (uint8_t)v;
         else if (FMT == 1) reinterpret_cast<uint16_t *>(row)[e] = (uint16_t)v;
         else reinterpret_cast<uint32_t *>(row)[e] = v;
@@ -542,8 +578,8 @@ __device__ __forceinline__ void obs_elems(const ObsLds &L, uint8_t *row, int e, 
 
 // Stream the 91,613-element row to `row` (element phase m) in 16-byte chunks:
 // chunk q covers row bytes [16q - lead, 16q - lead + 16).
-template <int FMT>
-__device__ void obs_emit(const ObsLds &L, uint8_t *row, int m)
+template <int FMT, bool EXT = false>
+__device__ void obs_emit(const ObsLds &L, uint8_t *row, int m, const ExtLds *X = nullptr)
 {
     constexpr int ES = FMT == 0 ? 4 : FMT == 1 ? 2 : 1;
     constexpr int EPC = 16 / ES;
@@ -560,8 +596,9 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m)
         const int q = qb + lane;
         const int e0 = q * EPC - m;
         uint8_t *dst = row + (ptrdiff_t)e0 * ES;
-        if (FMT != 2 && ((s_lo < CT0_E && s_hi > CT0_S) || (s_lo < CT1_E && s_hi > CT1_S))) {
-            if (q < ql) obs_elems<FMT>(L, row, e0, e0 + EPC, m);
+        if (FMT != 2 && ((s_lo < CT0_E && s_hi > CT0_S) || (s_lo < CT1_E && s_hi > CT1_S) ||
+                         (EXT && ((s_lo < EB0_E && s_hi > EB0_S) || (s_lo < EB1_E && s_hi > EB1_S))))) {
+            if (q < ql) obs_elems<FMT, EXT>(L, row, e0, e0 + EPC, m, X);
             continue;
         }
         int nov = 0, d = 0, rs = 0, re = 0;
@@ -586,8 +623,8 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m)
         *reinterpret_cast<uint4 *>(dst) = out;
     }
     // partial chunks at the two ends of the row
-    if (threadIdx.x == 0 && lead) obs_elems<FMT>(L, row, 0, EPC - m, m);
-    if (threadIdx.x == 64 && ((NBYTES + lead) & 15)) obs_elems<FMT>(L, row, ql * EPC - m, OBS_ROW, m);
+    if (threadIdx.x == 0 && lead) obs_elems<FMT, EXT>(L, row, 0, EPC - m, m, X);
+    if (threadIdx.x == 64 && ((NBYTES + lead) & 15)) obs_elems<FMT, EXT>(L, row, ql * EPC - m, OBS_ROW, m, X);
 }
 
 // Image offset of the u8 chunk starting at element e0: inside the range it
@@ -669,13 +706,21 @@ __device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m
 }
 
 // nrows = N (one row per env, observer given or the acting seat) or 4N
-// (all_seats: row = env * 4 + observer). One 256-thread block per row.
-template <int FMT>
+// (all_seats: row = env * 4 + observer). One 256-thread block per row. EXT
+// (f32 / bf16): belief planes from ext, (N, 4, 12, 289) float32 world-cell
+// beliefs per (env, observer).
+template <int FMT, bool EXT = false>
 __global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *__restrict__ observer, int all_seats,
                                                          void *__restrict__ spatial, float *__restrict__ aux,
-                                                         float *__restrict__ glob, int nrows)
+                                                         float *__restrict__ glob, int nrows,
+                                                         const float *__restrict__ ext = nullptr)
 {
     __shared__ ObsLds L;
+    ExtLds *X = nullptr;
+    if constexpr (EXT) {
+        __shared__ ExtLds XL;
+        X = &XL;
+    }
     constexpr int ES = FMT == 0 ? 4 : FMT == 1 ? 2 : 1;
     const int t = threadIdx.x, row = blockIdx.x;
     if (row >= nrows) return;
@@ -684,13 +729,15 @@ __global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *
     const int m = (int)(((uintptr_t)rowp / ES) & (16 / ES - 1));
     obs_setup(L, t, OBS_THREADS);
     obs_clear(L, t, OBS_THREADS);
+    if (EXT && t < PID_STRIDE) X->rel[t] = 0;
     lds_barrier();
     RowIn R;
     row_fetch(S, env, obs, t, R);
-    row_fill(S, obs, m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr);
+    row_fill<EXT>(S, obs, m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr,
+                  EXT ? ext + ((size_t)env * 4 + obs) * 12 * NC : nullptr, X);
     lds_barrier();
     if (FMT == 2) obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUX_ROW : nullptr, t);
-    else obs_emit<FMT>(L, rowp, m);
+    else obs_emit<FMT, EXT>(L, rowp, m, X);
 }
 
 // u8, persistent single-buffer form: 256 threads, one LDS row. Per row: fill

@@ -219,9 +219,21 @@ class GpuRollout:
         self._observer_seats = torch.from_numpy(a.astype(np.int8)).to(self.device).contiguous()
 
     def upload_beliefs(self, beliefs: np.ndarray) -> None:
-        raise NotImplementedError(
-            "beliefs are maintained on the device with BeliefTensor semantics (info_model.py:218-429); "
-            "external (N,4,12,289) belief inputs are not supported by this build")
+        """Replace the beliefs the observations read (gpu_rollout.py:966-981):
+        (N, 4, 12, 289) float32 world-cell beliefs per (env, observer); the
+        belief planes take the observer's value at each teammate / enemy piece's
+        cell. Until then (and after ``clear_beliefs``) the device's own
+        BeliefTensor beliefs are used."""
+        if beliefs.shape != (self.num_envs, 4, 12, 289):
+            raise ValueError(f"beliefs shape must be ({self.num_envs}, 4, 12, 289), got {beliefs.shape}")
+        if beliefs.dtype != np.float32:
+            beliefs = beliefs.astype(np.float32, copy=False)
+        self._beliefs = beliefs
+        self._b.upload_beliefs(beliefs)
+
+    def clear_beliefs(self) -> None:
+        self._beliefs = None
+        self._b.clear_beliefs()
 
     # ------------------------------------------------------------ termination, views
     def read_termination(self) -> dict[str, np.ndarray]:

@@ -120,10 +120,9 @@ class GpuWorld:
     def build_observation(self, beliefs: np.ndarray | None = None, observer_seats: np.ndarray | None = None,
                           show_mode: int = 2) -> tuple[np.ndarray, np.ndarray]:
         """(N,4,317,17,17) and (N,4,28) float32 on the host (gpu_world.py:276-293).
-        Beliefs come from the device's own BeliefTensor state, so `beliefs` must
-        be None; `show_mode` must be the mode the world was created with."""
-        if beliefs is not None:
-            raise NotImplementedError("external belief inputs are not supported by this build")
+        `beliefs` (N,4,12,289) float32 world-cell beliefs feed the belief planes
+        of this call (None: the device's own BeliefTensor beliefs); `show_mode`
+        must be the mode the world was created with."""
         if _show_value(show_mode) != self.state.show_mode:
             raise ValueError(f"show_mode {show_mode} differs from the world's show mode {self.state.show_mode}")
         obs = None
@@ -132,8 +131,14 @@ class GpuWorld:
             if a.shape != (self.num_envs, 4):
                 raise ValueError(f"observer_seats shape must be ({self.num_envs}, 4), got {a.shape}")
             obs = torch.from_numpy(a.astype(np.int8)).to(self.device)
-        sp, gl = self.state.observe(obs, fmt="f32", all_seats=True)
-        return sp.cpu().numpy(), gl.cpu().numpy()
+        if beliefs is not None:
+            self.state.upload_beliefs(np.asarray(beliefs, dtype=np.float32))
+        try:
+            sp, gl = self.state.observe(obs, fmt="f32", all_seats=True)
+            return sp.cpu().numpy(), gl.cpu().numpy()
+        finally:
+            if beliefs is not None:
+                self.state.clear_beliefs()
 
     def release_scratch(self) -> None:
         """No per-call scratch exists (all buffers belong to the handle)."""

@@ -1026,7 +1026,25 @@ static int in_back_two(int seat, int zx, int zy)
     }
 }
 
-void jqo_observe(const jqo_game *g, int obs, float *out, float *glob)
+/* ext == NULL: belief planes from the BeliefTensor codes. Otherwise ext is the
+ * observer's uploaded (12, 289) belief slice in world cells, read at each
+ * teammate / enemy piece's cell where it is > 0 (the reference's uploaded-belief
+ * path, src/env/cuda/src/observation.cu:246-372). */
+static void observe_impl(const jqo_game *g, int obs, const float *ext, float *out, float *glob);
+
+void jqo_observe(const jqo_game *g, int obs, float *out, float *glob) { observe_impl(g, obs, NULL, out, glob); }
+
+void jqo_observe_ext(const jqo_game *g, int obs, const float *ext, float *out, float *glob)
+{
+    observe_impl(g, obs, ext, out, glob);
+}
+
+static void ext_row(const float *ext, int f, float out[12])
+{
+    for (int t = 0; t < 12; t++) out[t] = ext[t * NC + f] > 0.f ? ext[t * NC + f] : 0.f;
+}
+
+static void observe_impl(const jqo_game *g, int obs, const float *ext, float *out, float *glob)
 {
     static const int CH_OWN = 0, CH_PTM = 12, CH_DTM = 24, CH_LE = 25, CH_RE = 26, CH_BL = 27, CH_BR = 39,
         CH_DEAD = 51, CH_FLAG = 54, CH_STATIC = 58, CH_TURN = 64, CH_MOVEB = 66, CH_EATB = 74, CH_SURVB = 82,
@@ -1042,12 +1060,16 @@ void jqo_observe(const jqo_game *g, int obs, float *out, float *glob)
         if (!g->alive[pid]) continue;
         int f = g->pos_y[pid] * 17 + g->pos_x[pid], s = g->pseat[pid], ti = tracked_idx(g->ptype[pid]);
         if (s == obs && ti >= 0) W(CH_OWN + ti, f) = 1.f;
-        if (s == tm) { jqo_belief_row(g->bcode[obs][pid], brow); for (int t = 0; t < 12; t++) W(CH_PTM + t, f) = brow[t]; }
+        if (s == tm || s == le || s == re) {
+            if (ext) ext_row(ext, f, brow);
+            else jqo_belief_row(g->bcode[obs][pid], brow);
+        }
+        if (s == tm) for (int t = 0; t < 12; t++) W(CH_PTM + t, f) = brow[t];
         if (g->show_mode == JQO_DARKMODE && s == tm) W(CH_DTM, f) = 1.f;
         if (s == le) W(CH_LE, f) = 1.f;
         if (s == re) W(CH_RE, f) = 1.f;
-        if (s == le) { jqo_belief_row(g->bcode[obs][pid], brow); for (int t = 0; t < 12; t++) W(CH_BL + t, f) = brow[t]; }
-        if (s == re) { jqo_belief_row(g->bcode[obs][pid], brow); for (int t = 0; t < 12; t++) W(CH_BR + t, f) = brow[t]; }
+        if (s == le) for (int t = 0; t < 12; t++) W(CH_BL + t, f) = brow[t];
+        if (s == re) for (int t = 0; t < 12; t++) W(CH_BR + t, f) = brow[t];
         int ours = (s & 1) == team, half = ours ? 0 : 4;
         int mb = g->move_count[pid] < 3 ? g->move_count[pid] : 3;
         W(CH_MOVEB + half + mb, f) = 1.f;

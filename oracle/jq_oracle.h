@@ -108,6 +108,10 @@ int  jqo_has_legal(const jqo_game *g, int seat);
 int  jqo_step(jqo_game *g, int src, int dst, jqo_result *res);
 int  jqo_move_requires_gongb(const jqo_game *g, int src, int dst);
 void jqo_observe(const jqo_game *g, int observer, float *spatial /*317*289*/, float *glob /*28*/);
+/* The same with the belief planes (12-23, 27-50) taken from the observer's
+ * uploaded (12, 289) world-cell belief slice: value at each teammate / enemy
+ * piece's cell where > 0 (observation.cu:246-372); globals unchanged. */
+void jqo_observe_ext(const jqo_game *g, int observer, const float *ext /*12*289*/, float *spatial, float *glob);
 uint64_t jqo_recompute_zobrist(const jqo_game *g);
 void jqo_belief_row(int code, float out[12]);
 

@@ -92,6 +92,7 @@ def lib() -> C.CDLL:
     L.jqo_step.argtypes = [P, C.c_int, C.c_int, P]; L.jqo_step.restype = C.c_int
     L.jqo_move_requires_gongb.argtypes = [P, C.c_int, C.c_int]; L.jqo_move_requires_gongb.restype = C.c_int
     L.jqo_observe.argtypes = [P, C.c_int, P, P]
+    L.jqo_observe_ext.argtypes = [P, C.c_int, P, P, P]
     L.jqo_recompute_zobrist.argtypes = [P]; L.jqo_recompute_zobrist.restype = C.c_uint64
     L.jqo_belief_row.argtypes = [C.c_int, P]
     L.jqo_sizeof_game.restype = C.c_int
@@ -211,10 +212,16 @@ class Game:
     def step_id(self, action_id: int) -> tuple[int, dict]:
         return self.step(action_id // NC, action_id % NC)
 
-    def observe(self, observer: int) -> tuple[np.ndarray, np.ndarray]:
+    def observe(self, observer: int, beliefs: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+        """Observation of `observer`; `beliefs` (12, 289) float32 world-cell
+        beliefs of that observer replace the BeliefTensor belief planes."""
         sp = np.zeros((OBS_C, 17, 17), dtype=np.float32)
         gl = np.zeros(OBS_G, dtype=np.float32)
-        lib().jqo_observe(_p(self.buf), observer, _p(sp), _p(gl))
+        if beliefs is None:
+            lib().jqo_observe(_p(self.buf), observer, _p(sp), _p(gl))
+        else:
+            b = np.ascontiguousarray(beliefs, dtype=np.float32).reshape(12, 289)
+            lib().jqo_observe_ext(_p(self.buf), observer, _p(b), _p(sp), _p(gl))
         return sp, gl
 
     def recompute_zobrist(self) -> int:

@@ -220,3 +220,66 @@ def test_world_push_state_step_and_legal(jq):
     assert not w.step_batch(np.zeros(n, np.int32))["valid"].any()
     assert term["terminated"].dtype == bool
     w.state.close()
+
+
+def test_uploaded_beliefs_feed_the_observation(jq):
+    """upload_beliefs (gpu_rollout.py:966-981): the belief planes take the
+    observer's uploaded value at each teammate / enemy piece's cell (> 0 only),
+    bit-exact against the oracle's uploaded-belief observation, for the acting
+    seat, every seat, bf16 and GpuWorld.build_observation; u8 is refused and
+    clear_beliefs returns to the BeliefTensor planes."""
+    from tests.test_gpu import _bf16_rne
+    n, show = 10, 2
+    ro = jq.GpuRollout(n, show_mode=show)
+    ro.reset(21)
+    games = G.oracle_games_from_lineups(jq.generate_lineups(21, n), show)
+    rng = np.random.default_rng(8)
+    for _ in range(25):
+        ids, counts = ro.legal_actions_dense(ro.turn_torch().cpu().numpy())
+        acts = np.array([ids[i, rng.integers(counts[i])] if counts[i] else -1 for i in range(n)], np.int32)
+        ro.step(acts)
+        for i, g in enumerate(games):
+            if acts[i] >= 0:
+                g.step_id(int(acts[i]))
+    bel = (rng.random((n, 4, 12, 289), dtype=np.float32) - np.float32(0.25)).astype(np.float32)
+    ro.upload_beliefs(bel)
+    acting = ro.turn_torch().clone()
+    sp, gl = ro.build_acting_seat_observation_torch(acting)
+    sp, gl = sp.cpu().numpy(), gl.cpu().numpy()
+    for i, g in enumerate(games):
+        seat = int(g.turn)
+        osp, ogl = g.observe(seat, bel[i, seat])
+        assert np.array_equal(sp[i].view(np.uint32), osp.view(np.uint32)), i
+        assert np.array_equal(gl[i], ogl), i
+    sp4, _ = ro.build_all_seat_observations()
+    for i, g in enumerate(games):
+        for k in range(4):
+            assert np.array_equal(sp4[i, k], g.observe(k, bel[i, k])[0]), (i, k)
+    bf, _ = ro.state.observe(acting, fmt="bf16")
+    bf = bf.view(torch.int16).cpu().numpy().view(np.uint16)
+    for i, g in enumerate(games):
+        assert np.array_equal(bf[i], _bf16_rne(g.observe(int(g.turn), bel[i, int(g.turn)])[0])), i
+    with pytest.raises(jq.JunqiError):
+        ro.state.observe(acting, fmt="u8")
+    ro.clear_beliefs()
+    sp, _ = ro.build_acting_seat_observation_torch(acting)
+    for i, g in enumerate(games):
+        assert np.array_equal(sp[i].cpu().numpy(), g.observe(int(g.turn))[0]), i
+    with pytest.raises(ValueError):
+        ro.upload_beliefs(bel[:, :3])
+    ro.close()
+    # GpuWorld: beliefs for one call only. The pushed state carries no combat
+    # memory (as push_state_from_envs in the reference), so only the belief
+    # planes are compared with the oracle; the others equal the world's own
+    # observation without uploaded beliefs.
+    w = jq.GpuWorld(n, show_mode=show)
+    w.push_state_from_envs(_fake_envs(games))
+    wsp, _ = w.build_observation(bel, show_mode=show)
+    wsp0, _ = w.build_observation(None, show_mode=show)
+    planes = list(range(12, 24)) + list(range(27, 51))
+    other = [c for c in range(317) if c not in planes]
+    for i, g in enumerate(games):
+        for k in range(4):
+            assert np.array_equal(wsp[i, k][planes], g.observe(k, bel[i, k])[0][planes]), (i, k)
+            assert np.array_equal(wsp[i, k][other], wsp0[i, k][other]), (i, k)
+    w.state.close()

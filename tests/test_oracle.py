@@ -365,3 +365,64 @@ def test_belief_prior_rows():
     assert np.isclose(O.belief_row(16 + 10).sum(), 1.0) and O.belief_row(16 + 10)[1] == 0
     assert O.belief_row(16 + 20)[1] == np.float32(3) / np.float32(24)
     assert np.all(O.belief_row(64) == np.float32(1.0 / 12.0))
+
+
+def _played_game(seed: int, plies: int, show: int = 2):
+    g = O.Game(O.random_setup(seed), show_mode=show)
+    rng = np.random.default_rng(seed)
+    for _ in range(plies):
+        ids = g.legal_ids()
+        if not len(ids) or g.terminated:
+            break
+        g.step_id(int(ids[rng.integers(len(ids))]))
+    return g
+
+
+def _projected_beliefs(g, obs: int) -> np.ndarray:
+    """The BeliefTensor rows of `obs` projected onto the cells of the pieces
+    they describe (every teammate / enemy piece on the board), as a world-cell
+    (12, 289) tensor."""
+    b = g.buf[0]
+    ext = np.zeros((12, 289), np.float32)
+    for pid in range(120):
+        s = int(b["pseat"][pid])
+        if b["alive"][pid] and s != obs:
+            f = int(b["pos_y"][pid]) * 17 + int(b["pos_x"][pid])
+            ext[:, f] = O.belief_row(int(b["bcode"][obs][pid]))
+    return ext
+
+
+@pytest.mark.parametrize("seed,plies,show", [(1, 0, 2), (7, 60, 2), (11, 140, 1), (5, 90, 0)])
+def test_uploaded_beliefs_oracle_is_pinned(seed, plies, show):
+    """jqo_observe_ext: (1) the BeliefTensor rows projected onto the piece
+    cells reproduce the ordinary observation (itself pinned by the reference's
+    obs hashes) bit for bit; (2) values away from piece cells do not matter;
+    (3) non-positive values read as 0; (4) doubling the tensor doubles exactly
+    the belief planes and nothing else."""
+    g = _played_game(seed, plies, show)
+    for obs in range(4):
+        sp0, gl0 = g.observe(obs)
+        ext = _projected_beliefs(g, obs)
+        sp1, gl1 = g.observe(obs, ext)
+        assert np.array_equal(sp1.view(np.uint32), sp0.view(np.uint32)) and np.array_equal(gl1, gl0)
+        rng = np.random.default_rng(seed * 4 + obs)
+        rnd = rng.random((12, 289), dtype=np.float32)
+        b = g.buf[0]
+        piece_cells = {int(b["pos_y"][p]) * 17 + int(b["pos_x"][p]) for p in range(120)
+                       if b["alive"][p] and int(b["pseat"][p]) != obs}
+        off = np.array([f for f in range(289) if f not in piece_cells])
+        noisy = rnd.copy()
+        noisy[:, off] = rng.random((12, len(off)), dtype=np.float32)
+        spa, gla = g.observe(obs, rnd)
+        spb, _ = g.observe(obs, noisy)
+        assert np.array_equal(spa, spb) and np.array_equal(gla, gl0)
+        neg = -rnd
+        spn, _ = g.observe(obs, neg)
+        bel = list(range(12, 24)) + list(range(27, 51))
+        assert not spn[bel].any()
+        other = [c for c in range(317) if c not in bel]
+        assert np.array_equal(spn[other], sp0[other]) and np.array_equal(spa[other], sp0[other])
+        sp2, _ = g.observe(obs, 2 * rnd)
+        assert np.array_equal(sp2[bel], 2 * spa[bel]) and np.array_equal(sp2[other], sp0[other])
+        # every value lands on a piece of the matching relation and nowhere else
+        assert np.count_nonzero(spa[bel]) == 12 * len(piece_cells) - np.count_nonzero(rnd[:, sorted(piece_cells)] == 0)
