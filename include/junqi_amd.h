@@ -28,6 +28,7 @@ extern "C" {
 #define JQ_MASK_WORDS 521          /* 32-bit words per packed canonical mask row */
 #define JQ_AUX_PLANES 6            /* continuous planes carried in fp32 by the u8 format */
 #define JQ_MAX_LEGAL 3200          /* per-env upper bound on legal actions (25 pieces x 128) */
+#define JQ_SLOTS_PER_PIECE 80      /* per-piece legal slot mask width (game_state.cu:1969) */
 
 /* error codes */
 #define JQ_OK 0
@@ -115,6 +116,17 @@ int jq_step(jq_env *env, const int32_t *actions, const int8_t *acting, int32_t a
  * legal_mask_canonical_batch (game_state.cu:2291-2508). */
 int jq_legal(jq_env *env, const int8_t *acting, int32_t *counts, int32_t *offsets, int32_t *values,
              int32_t *mask_words, uint8_t *mask_bool, void *stream);
+
+/* Per-piece slot mask of `acting` (device int8 N; NULL = current turn):
+ * slots: device uint8 (N, 120, 80), 16-byte aligned; slots[i][pid][s] = 1 iff
+ * piece pid can take slot s. Slots 0-3 road steps (+x,-x,+y,-y), 4-7 camp
+ * diagonals, 8-55 a non-engineer's straight rail runs (8 + dir*12 + k), 56-67
+ * its curve-rail destinations, an engineer's rail destinations from slot 8;
+ * the two BFS sections are packed from their first slot. Each piece row holds
+ * as many ones as that piece has legal moves. Replaces legal_action_mask_batch
+ * (bindings.cpp:951-990, game_state.cu:1964-2197; gpu_world.py:208-217,
+ * gpu_rollout.py:862-869). */
+int jq_legal_slots(jq_env *env, const int8_t *acting, uint8_t *slots, void *stream);
 
 /* Observation of `observer` (device int8 N; NULL = current turn) in that seat's
  * canonical frame. fmt JQ_OBS_*; spatial: device (N,317,17,17) of the format's

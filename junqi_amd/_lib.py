@@ -16,12 +16,14 @@ OBS_F32, OBS_BF16, OBS_U8 = 0, 1, 2
 ACT_WORLD, ACT_CANONICAL = 0, 1
 NUM_CELLS = 289
 NUM_ON_BOARD = 129
+NUM_PIDS = 120
 ACTION_DIM = 16641
 MASK_WORDS = 521
 OBS_CHANNELS = 317
 OBS_GLOBALS = 28
 AUX_PLANES = 6
 MAX_LEGAL = 3200
+SLOTS_PER_PIECE = 80
 AUX_CHANNELS = (64, 65, 253, 254, 255, 256)
 
 FIELDS = {
@@ -38,7 +40,7 @@ _EXPORTS = [
     "jq_last_error", "jq_version", "jq_create", "jq_destroy", "jq_num_envs", "jq_upload_zobrist",
     "jq_upload_recency", "jq_upload_setup_pool", "jq_reset_lineups", "jq_reset_seeded",
     "jq_generate_lineups", "jq_generate_pool", "jq_board_tables", "jq_reset_terminated", "jq_step",
-    "jq_legal", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_env_step",
+    "jq_legal", "jq_legal_slots", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_env_step",
     "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import", "jq_rehash",
     "jq_sync", "jq_history_create", "jq_history_destroy", "jq_history_bytes", "jq_history_snapshot",
     "jq_history_reconstruct", "jq_mask_count", "jq_mask_to_ids", "jq_ids_to_mask", "jq_upload_beliefs",
@@ -72,6 +74,7 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_reset_terminated": ([P, I64, P], C.c_int),
         "jq_step": ([P, P, P, I32, P, P, P, P, P, P, P, P, P, P], C.c_int),
         "jq_legal": ([P, P, P, P, P, P, P, P], C.c_int),
+        "jq_legal_slots": ([P, P, P, P], C.c_int),
         "jq_observe": ([P, P, I32, I32, P, P, P, P], C.c_int),
         "jq_obs_decode_table": ([P], C.c_int),
         "jq_sample_uniform": ([P, P, P, P, U64, U64, P, P], C.c_int),

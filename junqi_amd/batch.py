@@ -196,6 +196,18 @@ class JunqiBatch:
             out["mask_bool"] = mb
         return out
 
+    def legal_slots(self, acting: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """(N, 120, 80) bool per-piece slot mask of the acting seats (legal_action_mask_batch,
+        game_state.cu:1964-2197)."""
+        s = None if acting is None else acting.to(device=self.device, dtype=torch.int8).contiguous()
+        shape = (self.n, L.NUM_PIDS, L.SLOTS_PER_PIECE)
+        if out is None:
+            out = torch.empty(shape, dtype=torch.bool, device=self.device)
+        elif tuple(out.shape) != shape or out.dtype != torch.bool or not out.is_contiguous():
+            raise ValueError(f"slot mask output must be a contiguous bool tensor of shape {shape}")
+        check(lib.jq_legal_slots(self._h, self._ptr(s), out.data_ptr(), self.stream))
+        return out
+
     def legal_csr_numpy(self, acting: torch.Tensor | None = None) -> tuple[np.ndarray, np.ndarray]:
         self.legal(acting, csr=True, mask_words=False)
         offsets = self.offsets.cpu().numpy()

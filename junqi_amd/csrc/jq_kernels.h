@@ -1202,6 +1202,91 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
     }
 }
 
+// ------------------------------------------------------------------ slot mask
+// Per-piece 80-slot legal mask (game_state.cu:1964-2197) from the legal sets
+// k_legal left in S.lg. Slots 0-3 are the road steps in table order, 4-7 the
+// camp diagonals, 8 + dir*12 + k the k-th cell of a non-engineer's straight
+// rail run (road neighbours of the source excepted, they sit in 0-3). The
+// reference packs curve-rail destinations (56..67) and an engineer's rail
+// destinations (8..79) contiguously in its BFS order, so those sections are a
+// run of ones as long as the destinations the earlier slots leave over.
+constexpr int JQ_SLOTS = 80;
+constexpr int JQ_SLOT_ROW = NP * JQ_SLOTS;   // bytes per env
+
+__device__ __forceinline__ void set_run(uint64_t &lo, uint32_t &hi, int a, int len)
+{   // bits [a, a + len) of the 80-bit slot set, a + len <= 80
+    if (len <= 0) return;
+    const int e = a + len;
+    if (a < 64) {
+        const int n = (e < 64 ? e : 64) - a;
+        lo |= (n == 64 ? ~0ull : ((1ull << n) - 1)) << a;
+    }
+    if (e > 64) {
+        const int ha = a > 64 ? a - 64 : 0;
+        hi |= ((1u << (e - 64 - ha)) - 1) << ha;
+    }
+}
+
+__device__ __forceinline__ uint32_t nibble_bytes(uint32_t nib)
+{   // 4 bits -> 4 bytes of 0 / 1
+    return (nib * 0x00204081u) & 0x01010101u;
+}
+
+__global__ __launch_bounds__(64) void k_slots(State S, uint8_t *__restrict__ out)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    __shared__ uint4 rows[30][JQ_SLOTS / 16];   // the acting seat's 30 piece rows
+    const LegalRec &G = S.lg[env];
+    const int n = G.n, seat = G.seat;
+    for (int q = l; q < 30 * (JQ_SLOTS / 16); q += 64) rows[q / 5][q % 5] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    const int src = l < n ? G.src[l] : -1;
+    const int pid = (unsigned)src < (unsigned)NC ? S.cell[(size_t)env * CELL_STRIDE + src] : -1;
+    if (l < n && (unsigned)(pid - seat * 30) < 30u) {   // a consistent state always passes
+        const BB M{G.mask[l][0], G.mask[l][1], G.mask[l][2]};
+        const bool eng = S.piece[pc_idx(env, pid)].ptype == T_GONGB;
+        uint64_t lo = 0;
+        uint32_t hi = 0;
+        int a[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[k] = cT.adj[src][k];
+            if (a[k] >= 0 && bb_has(M, cT.f2c[a[k]])) lo |= 1ull << k;
+            const int d = cT.diag[src][k];
+            if (d >= 0 && bb_has(M, cT.f2c[d])) lo |= 1ull << (4 + k);
+        }
+        const int total = __popcll(M.w0) + __popcll(M.w1) + __popcll(M.w2);
+        const int r = cT.railidx[src];
+        if (r >= 0 && !eng) {
+            for (int d = 0; d < 4; ++d)
+                for (int k = 0; k < cT.raylen[r][d]; ++k) {
+                    const int f = cT.rays[r][d][k];
+                    if (f != a[0] && f != a[1] && f != a[2] && f != a[3] && bb_has(M, cT.f2c[f]))
+                        lo |= 1ull << (8 + d * 12 + k);
+                }
+            const int rest = total - __popcll(lo);
+            set_run(lo, hi, 56, rest < 12 ? rest : 12);
+        } else if (r >= 0) {
+            const int rest = total - __popcll(lo);
+            set_run(lo, hi, 8, rest < 72 ? rest : 72);
+        }
+        uint4 *row = rows[pid - seat * 30];
+#pragma unroll
+        for (int j = 0; j < JQ_SLOTS / 16; ++j) {
+            const uint32_t b = j < 4 ? (uint32_t)(lo >> (16 * j)) & 0xFFFFu : hi & 0xFFFFu;
+            row[j] = make_uint4(nibble_bytes(b & 0xF), nibble_bytes((b >> 4) & 0xF),
+                                nibble_bytes((b >> 8) & 0xF), nibble_bytes(b >> 12));
+        }
+    }
+    __syncthreads();
+    uint4 *dst = reinterpret_cast<uint4 *>(out + (size_t)env * JQ_SLOT_ROW);
+    for (int q = l; q < JQ_SLOT_ROW / 16; q += 64) {
+        const int p = q / 5 - seat * 30;
+        dst[q] = (n > 0 && (unsigned)p < 30u) ? rows[p][q % 5] : make_uint4(0, 0, 0, 0);
+    }
+}
+
 // ------------------------------------------------------------------ sampler
 __device__ __forceinline__ uint32_t philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
                                                  uint32_t k0, uint32_t k1)

@@ -402,6 +402,18 @@ int jq_legal(jq_env *e, const int8_t *acting, int32_t *counts, int32_t *offsets,
     return JQ_OK;
 }
 
+int jq_legal_slots(jq_env *e, const int8_t *acting, uint8_t *slots, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!slots) return fail(JQ_E_ARG, "null slot mask");
+    if ((uintptr_t)slots % 16) return fail(JQ_E_ARG, "slot mask must be 16-byte aligned");
+    hipLaunchKernelGGL(k_legal, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, acting, nullptr, nullptr, nullptr);
+    if ((rc = launch_check("k_legal")) != 0) return rc;
+    hipLaunchKernelGGL(k_slots, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, slots);
+    return launch_check("k_slots");
+}
+
 int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial, float *aux,
                float *global, void *stream)
 {

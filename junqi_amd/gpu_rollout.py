@@ -161,9 +161,10 @@ class GpuRollout:
         return ids.cpu().numpy(), counts.cpu().numpy()
 
     def legal_actions_mask(self, acting_seats: np.ndarray) -> np.ndarray:
-        raise NotImplementedError(
-            "the per-piece slot mask (game_state.cu:1985-2197) encodes the reference kernel's own rail "
-            "traversal order; use legal_mask_canonical_torch[_device] or legal_actions_dense")
+        """(N, 120, 80) bool per-piece slot mask (gpu_rollout.py:862-869): slot
+        layout of legal_action_mask_batch (game_state.cu:1964-2197)."""
+        s = torch.from_numpy(self._seats_np(acting_seats)).to(self.device)
+        return self._b.legal_slots(s).cpu().numpy()
 
     def legal_mask_canonical_torch(self, acting_seats: np.ndarray | None = None) -> torch.Tensor:
         """(N, 16641) bool device mask over compact canonical ids

@@ -93,9 +93,10 @@ class GpuWorld:
         return self.state.legal_csr_numpy(torch.from_numpy(acting_seats).to(self.device))
 
     def legal_actions_mask(self, acting_seats: np.ndarray) -> np.ndarray:
-        raise NotImplementedError(
-            "the per-piece slot mask (game_state.cu:1985-2197) encodes the reference kernel's own rail "
-            "traversal order; use legal_actions_csr / legal_actions_dense or GpuRollout's canonical mask")
+        """(N, 120, 80) bool per-piece slot mask (gpu_world.py:208-217): slot
+        layout of legal_action_mask_batch (game_state.cu:1964-2197)."""
+        self._validate_acting_seats(acting_seats)
+        return self.state.legal_slots(torch.from_numpy(acting_seats).to(self.device)).cpu().numpy()
 
     # ------------------------------------------------------------ step
     def step_batch(self, action_ids: np.ndarray) -> dict:

@@ -488,6 +488,76 @@ int jqo_has_legal(const jqo_game *g, int seat)
     return legal_ids_raw(g, seat, tmp) > 0;
 }
 
+/* Rail BFS from src over the sorted rail graph, visiting each cell once; a
+ * cell that passes `keep` is enqueued when empty. Destinations that are
+ * landable and not filtered out by `skip` go to slots [*cur, end).
+ * (game_state.cu:2077-2124 with keep = same curve, skip = same axis;
+ *  game_state.cu:2150-2195 with keep = all, skip = road neighbour of src) */
+static void slot_bfs(const jqo_game *g, int src, int team, int curve_only, uint8_t *row, int *cur, int end)
+{
+    uint8_t vis[NC] = {0}; int16_t q[NC]; int qh = 0, qt = 0;
+    const int sx = src % 17, sy = src / 17;
+    vis[src] = 1; q[qt++] = (int16_t)src;
+    while (qh < qt) {
+        int c = q[qh++];
+        for (int a = 0; a < T_nradj[c]; a++) {
+            int nb = T_radj[c][a];
+            if (vis[nb]) continue;
+            vis[nb] = 1;
+            if (curve_only && T_curve[nb] != T_curve[src]) continue;
+            int skip;
+            if (curve_only) skip = (nb % 17 == sx) || (nb / 17 == sy);
+            else skip = nb == T_adj[src][0] || nb == T_adj[src][1] || nb == T_adj[src][2] || nb == T_adj[src][3];
+            if (!occupied(g, nb)) {
+                if (!skip && *cur < end) row[(*cur)++] = 1;
+                q[qt++] = (int16_t)nb;
+            } else if (!skip && *cur < end && enemy_att(g, nb, team)) {
+                row[(*cur)++] = 1;
+            }
+        }
+    }
+}
+
+int jqo_legal_slots(const jqo_game *g, int seat, uint8_t *out)
+{
+    memset(out, 0, (size_t)NP * JQO_SLOTS);
+    if (seat < 0 || seat > 3 || g->seat_dead[seat] || g->terminated) return 0;
+    const int team = seat & 1;
+    int total = 0;
+    for (int pid = 0; pid < NP; pid++) {   /* game_state.cu:2005-2018 gate */
+        if (!g->alive[pid] || g->pseat[pid] != seat) continue;
+        int t = g->ptype[pid];
+        if (t == JQO_JUNQI || t == JQO_DILEI) continue;
+        if (g->pos_x[pid] < 0 || g->pos_y[pid] < 0) continue;
+        int src = g->pos_y[pid] * 17 + g->pos_x[pid];
+        if (!T_on[src] || T_sh[src]) continue;
+        uint8_t *row = out + (size_t)pid * JQO_SLOTS;
+        for (int k = 0; k < 4; k++) {   /* game_state.cu:2032-2043 */
+            int nb = T_adj[src][k];
+            if (nb >= 0 && landable(g, nb, team)) row[k] = 1;
+        }
+        for (int k = 0; k < T_ndiag[src]; k++)
+            if (landable(g, T_diag[src][k], team)) row[4 + k] = 1;
+        if (T_rail[src]) {
+            if (t != JQO_GONGB) {   /* game_state.cu:2055-2075 */
+                for (int d = 0; d < 4; d++)
+                    for (int k = 0; k < T_nray[src][d]; k++) {
+                        int nb = T_ray[src][d][k];
+                        int ortho = nb == T_adj[src][0] || nb == T_adj[src][1] || nb == T_adj[src][2] || nb == T_adj[src][3];
+                        if (!occupied(g, nb)) { if (!ortho) row[8 + d * 12 + k] = 1; continue; }
+                        if (!ortho && enemy_att(g, nb, team)) row[8 + d * 12 + k] = 1;
+                        break;
+                    }
+                if (T_curve[src] > 0) { int cur = 56; slot_bfs(g, src, team, 1, row, &cur, 68); }
+            } else {
+                int cur = 8; slot_bfs(g, src, team, 0, row, &cur, JQO_SLOTS);
+            }
+        }
+        for (int s = 0; s < JQO_SLOTS; s++) total += row[s];
+    }
+    return total;
+}
+
 /* ---- legacy pairwise predicates (move_gen.py:127-376) ---- */
 static int straight_rail_clear(const jqo_game *g, int src, int dst)
 {   /* move_gen.py:127-171 */

@@ -24,6 +24,7 @@ extern "C" {
 #define JQO_OBS_C 317
 #define JQO_OBS_G 28
 #define JQO_ONB 129  /* on-board cells */
+#define JQO_SLOTS 80 /* per-piece legal slots (game_state.cu:1969) */
 
 /* PieceType values (junqi_core/rules.py:49-70) */
 enum { JQO_NONE = 0, JQO_DARK = 1, JQO_JUNQI = 2, JQO_DILEI = 3, JQO_ZHADAN = 4,
@@ -105,6 +106,12 @@ int  jqo_from_pieces(jqo_game *g, int n, const int32_t *pieces /* n x (pid, type
 int  jqo_is_legal(const jqo_game *g, int seat, int src, int dst);
 int  jqo_legal_ids(const jqo_game *g, int seat, int32_t *out, int cap);
 int  jqo_has_legal(const jqo_game *g, int seat);
+/* Per-piece 80-slot legal mask of `seat` (game_state.cu:1964-2197), out[120*80]:
+ * slots 0-3 road steps (+x,-x,+y,-y), 4-7 camp diagonals, 8-55 straight rail
+ * runs (dir*12 + k), 56-67 curve-rail destinations in BFS order, engineers'
+ * rail BFS destinations from slot 8. Zero for a dead seat or a finished game,
+ * like jqo_legal_ids. Returns the number of set slots. */
+int  jqo_legal_slots(const jqo_game *g, int seat, uint8_t *out);
 int  jqo_step(jqo_game *g, int src, int dst, jqo_result *res);
 int  jqo_move_requires_gongb(const jqo_game *g, int src, int dst);
 void jqo_observe(const jqo_game *g, int observer, float *spatial /*317*289*/, float *glob /*28*/);

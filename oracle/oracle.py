@@ -89,6 +89,7 @@ def lib() -> C.CDLL:
     L.jqo_is_legal.argtypes = [P, C.c_int, C.c_int, C.c_int]; L.jqo_is_legal.restype = C.c_int
     L.jqo_legal_ids.argtypes = [P, C.c_int, P, C.c_int]; L.jqo_legal_ids.restype = C.c_int
     L.jqo_has_legal.argtypes = [P, C.c_int]; L.jqo_has_legal.restype = C.c_int
+    L.jqo_legal_slots.argtypes = [P, C.c_int, P]; L.jqo_legal_slots.restype = C.c_int
     L.jqo_step.argtypes = [P, C.c_int, C.c_int, P]; L.jqo_step.restype = C.c_int
     L.jqo_move_requires_gongb.argtypes = [P, C.c_int, C.c_int]; L.jqo_move_requires_gongb.restype = C.c_int
     L.jqo_observe.argtypes = [P, C.c_int, P, P]
@@ -197,6 +198,13 @@ class Game:
         n = lib().jqo_legal_ids(_p(self.buf), seat, _p(out), 8192)
         assert n >= 0
         return out[:n].copy()
+
+    def legal_slots(self, seat: int | None = None) -> np.ndarray:
+        """(120, 80) bool per-piece slot mask (game_state.cu:1964-2197)."""
+        seat = int(self.buf[0]["turn"]) if seat is None else seat
+        out = np.zeros((120, 80), dtype=np.uint8)
+        lib().jqo_legal_slots(_p(self.buf), seat, _p(out))
+        return out.astype(bool)
 
     def is_legal(self, seat: int, src: int, dst: int) -> bool:
         return bool(lib().jqo_is_legal(_p(self.buf), seat, src, dst))

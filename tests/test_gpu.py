@@ -309,6 +309,53 @@ def test_engineer_stress_legal_sets(jq):
     b.close()
 
 
+def test_slot_mask_matches_oracle(jq):
+    """legal_action_mask_batch layout: device slot rows equal the oracle's for
+    every seat, during play (with resets) and on engineer-dense positions."""
+    n, seed = 48, 23
+    print(f"[slots] play n={n} seed={seed}", flush=True)
+    b = jq.JunqiBatch(n, show_mode=2, pool_size=64)
+    b.reset(seed)
+    games = G.oracle_games_from_lineups(jq.generate_lineups(seed, n), 2, 4000)
+    rng = np.random.default_rng(seed)
+    for ply in range(120):
+        if ply % 10 == 0:
+            for seat in range(4):
+                got = b.legal_slots(torch.full((n,), seat, dtype=torch.int8, device=b.device)).cpu().numpy()
+                for i, g in enumerate(games):
+                    assert np.array_equal(got[i], g.legal_slots(seat)), (ply, i, seat)
+        got = b.legal_slots().cpu().numpy()
+        offs, vals = b.legal_csr_numpy()
+        acts = np.full(n, -1, np.int32)
+        for i, g in enumerate(games):
+            assert np.array_equal(got[i], g.legal_slots()), (ply, i)
+            row = vals[offs[i]:offs[i + 1]]
+            assert int(got[i].sum()) == len(row)
+            if len(row):
+                acts[i] = row[rng.integers(len(row))]
+        b.step(torch.from_numpy(acts).to(b.device))
+        for i, g in enumerate(games):
+            if acts[i] >= 0:
+                g.step_id(int(acts[i]))
+        term = [i for i, g in enumerate(games) if g.terminated]
+        if term:
+            b.reset_terminated(ply)
+            for i in term:
+                games[i] = O.Game(b.pool[G.reset_pool_index(i, ply, b.pool.shape[0])], show_mode=2)
+    b.close()
+    positions = _engineer_positions(256, 9)
+    print(f"[slots] engineer positions n={len(positions)}", flush=True)
+    b = jq.JunqiBatch(len(positions), show_mode=2)
+    _import_positions(jq, b, positions)
+    games = [O.Game.from_pieces(p["pieces"], turn=p["turn"]) for p in positions]
+    out = torch.empty((b.n, 120, 80), dtype=torch.bool, device=b.device)
+    for seat in range(4):
+        got = b.legal_slots(torch.full((b.n,), seat, dtype=torch.int8, device=b.device), out=out).cpu().numpy()
+        for i, g in enumerate(games):
+            assert np.array_equal(got[i], g.legal_slots(seat)), (i, seat)
+    b.close()
+
+
 def test_invalid_actions_leave_state(jq):
     b = jq.JunqiBatch(8, show_mode=2)
     b.reset(3)

@@ -145,6 +145,11 @@ def test_rollout_dense_legal_and_reset_from_pool(jq):
         want = g.legal_ids(int(seats[i]))
         assert counts[i] == len(want)
         assert np.array_equal(ids[i, :counts[i]], want) and np.all(ids[i, counts[i]:] == -1)
+    m = ro.legal_actions_mask(seats)
+    assert m.shape == (n, 120, 80) and m.dtype == bool
+    for i, g in enumerate(games):
+        assert np.array_equal(m[i], g.legal_slots(int(seats[i]))), i
+        assert int(m[i].sum()) == counts[i]
     ro.reset_from_setup_pool(seed=9)
     pool = ro.batch.pool
     games = [O.Game(pool[G.reset_pool_index(i, 9, pool.shape[0])], show_mode=2) for i in range(n)]
@@ -212,8 +217,15 @@ def test_world_push_state_step_and_legal(jq):
                 o["flag_captured"]), (ply, i)
         z = w.state.get_field("zobrist")[:, 0]
         assert all(int(z[i]) == int(g.zobrist) for i, g in enumerate(games)), ply
+    seats = w.state.field_tensor("turn").cpu().numpy().astype(np.int8)
+    m = w.legal_actions_mask(seats)
+    assert m.shape == (n, 120, jq.SLOTS_PER_PIECE) and m.dtype == bool
+    for i, g in enumerate(games):
+        assert np.array_equal(m[i], g.legal_slots(int(seats[i]))), i
     with pytest.raises(ValueError):
         w.legal_actions_csr(np.zeros(n, np.int32))
+    with pytest.raises(ValueError):
+        w.legal_actions_mask(np.zeros(n, np.int32))
     term = w.pull_termination_state()
     w.push_termination_state(np.ones(n, bool), np.zeros(n, np.int8), np.zeros(n, bool))
     assert w.pull_termination_state()["terminated"].all()

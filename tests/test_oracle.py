@@ -426,3 +426,132 @@ def test_uploaded_beliefs_oracle_is_pinned(seed, plies, show):
         assert np.array_equal(sp2[bel], 2 * spa[bel]) and np.array_equal(sp2[other], sp0[other])
         # every value lands on a piece of the matching relation and nowhere else
         assert np.count_nonzero(spa[bel]) == 12 * len(piece_cells) - np.count_nonzero(rnd[:, sorted(piece_cells)] == 0)
+
+
+# ---------------------------------------------------------------- per-piece slot mask
+
+_OD = ((1, 0), (-1, 0), (0, 1), (0, -1))
+
+
+def _slot_geometry(t):
+    """Road neighbours, camp diagonals and straight rail runs per cell, from
+    coordinates and the exported rail graph (not the oracle's own tables)."""
+    on, camp = t["on_board"], t["camp"]
+    ra = np.asarray(t["rail_adj"]).reshape(289, 4)
+
+    def inside(x, y):
+        return 0 <= x < 17 and 0 <= y < 17 and on[y * 17 + x]
+
+    road, diag, runs = {}, {}, {}
+    for f in range(289):
+        if not on[f]:
+            continue
+        x, y = f % 17, f // 17
+        road[f] = [(y + dy) * 17 + x + dx if inside(x + dx, y + dy) else -1 for dx, dy in _OD]
+        diag[f] = [(y + dy) * 17 + x + dx for dx, dy in ((1, 1), (1, -1), (-1, 1), (-1, -1))
+                   if inside(x + dx, y + dy) and (camp[f] or camp[(y + dy) * 17 + x + dx])]
+        runs[f] = []
+        for dx, dy in _OD:
+            run, cur = [], f
+            while True:
+                nxt = [int(n) for n in ra[cur] if n >= 0 and (
+                    (dy == 0 and n // 17 == y and (n % 17 - cur % 17) * dx > 0)
+                    or (dx == 0 and n % 17 == x and (n // 17 - cur // 17) * dy > 0))]
+                if not nxt:
+                    break
+                cur = nxt[0]
+                run.append(cur)
+            runs[f].append(run)
+    return road, diag, runs
+
+
+def _slots_from_legal(g, seat, geo, t):
+    """The slot layout of legal_action_mask_batch (game_state.cu:1964-2197)
+    filled from the legal-id set: a slot is set iff its destination is legal;
+    the curve / engineer BFS sections are packed, so they hold as many leading
+    ones as the piece has destinations left over."""
+    road, diag, runs = geo
+    ids = g.legal_ids(seat)
+    out = np.zeros((120, 80), bool)
+    for pid in range(seat * 30, seat * 30 + 30):
+        if not g.alive[pid] or g.pos_x[pid] < 0:
+            continue
+        f = int(g.pos_y[pid]) * 17 + int(g.pos_x[pid])
+        dests = {int(i) % 289 for i in ids if i // 289 == f}
+        if not dests:
+            continue
+        for k, c in enumerate(road[f]):
+            out[pid, k] = c >= 0 and c in dests
+        for k, c in enumerate(diag[f]):
+            out[pid, 4 + k] = c in dests
+        if not t["rail"][f]:
+            continue
+        if g.ptype[pid] != 13:
+            for d, run in enumerate(runs[f]):
+                for k, c in enumerate(run):
+                    out[pid, 8 + d * 12 + k] = c in dests and c not in road[f]
+            rest = len(dests) - int(out[pid, :56].sum())
+            out[pid, 56:56 + rest] = True
+        else:
+            rest = len(dests) - int(out[pid, :8].sum())
+            out[pid, 8:8 + rest] = True
+    return out
+
+
+def _sparse_positions(n, seed):
+    t = O.tables()
+    on = [f for f in range(289) if t["on_board"][f]]
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        cells = list(rng.permutation(on))
+        pieces = []
+        for s in range(4):
+            kinds = rng.choice([4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 13, 13], size=rng.integers(1, 12))
+            for j, kd in enumerate(kinds):
+                f = int(cells.pop())
+                pieces.append((s * 30 + j, int(kd), f % 17, f // 17))
+        yield O.Game.from_pieces(pieces, turn=int(rng.integers(4)))
+
+
+def test_slot_mask_oracle_is_pinned():
+    """jqo_legal_slots against the legal-id enumeration (pinned by the golden
+    scenarios): every slot decodes to a legal destination through the board
+    geometry, BFS sections are packed runs, and per piece the set slots number
+    its legal moves (the reference's own invariants, tests/test_gpu_csr_mask.py
+    :162-249 and tests/test_gpu_engineer_adversarial.py:143-196), over played
+    games and sparse boards dense with engineers."""
+    t = O.tables()
+    geo = _slot_geometry(t)
+    states = [(g.clone(), int(g.turn)) for g, _ in _random_games(6, 260, seed0=40)]
+    states += [(g, s) for g in _sparse_positions(150, 3) for s in range(4)]
+    assert len(states) > 1000
+    for g, seat in states:
+        got = g.legal_slots(seat)
+        assert np.array_equal(got, _slots_from_legal(g, seat, geo, t))
+        ids = g.legal_ids(seat)
+        assert int(got.sum()) == len(ids)
+        others = np.ones(120, bool)
+        others[seat * 30:seat * 30 + 30] = False
+        assert not got[others].any()
+        eng = np.asarray(g.ptype) == 13
+        assert not got[~eng, 68:].any()
+        assert (got[:, 8:].sum(1) <= 72).all()
+
+
+@pytest.mark.parametrize("xy", [(8, 1), (6, 1), (8, 5), (8, 15), (1, 8), (15, 8)])
+def test_lone_engineer_slot_count(xy):
+    """tests/test_gpu_engineer_adversarial.py:143-160: the lone engineer's slot
+    row holds one slot per legal move; its rail section is one packed run."""
+    g = _lone(0, 13, xy)
+    row = g.legal_slots(0)[0]
+    assert int(row.sum()) == len(g.legal_ids(0))
+    n = int(row[8:].sum())
+    assert row[8:8 + n].all() and n <= 72
+
+
+def test_slot_mask_empty_for_dead_seat_and_finished_game():
+    g = _lone(0, 12, (8, 11))
+    assert g.legal_slots(0).any()
+    assert not g.legal_slots(1).any()   # no pieces
+    g.buf[0]["terminated"] = 1
+    assert not g.legal_slots(0).any()
