@@ -28,6 +28,9 @@ extern "C" {
 #define JQ_MASK_WORDS 521          /* 32-bit words per packed canonical mask row */
 #define JQ_AUX_PLANES 6            /* continuous planes carried in fp32 by the u8 format */
 #define JQ_MAX_LEGAL 3200          /* per-env upper bound on legal actions (25 pieces x 128) */
+/* setup styles for jq_generate_styled */
+#define JQ_SETUP_CANONICAL 1
+#define JQ_SETUP_MIXED 2
 #define JQ_SLOTS_PER_PIECE 80      /* per-piece legal slot mask width (game_state.cu:1969) */
 
 /* error codes */
@@ -85,6 +88,18 @@ int jq_generate_lineups(int64_t seed_base, int32_t count, int8_t *host_out);
 /* The setup pool of junqi_rl/gpu_rollout.py:255-275: pool_size setups drawn from
  * one random.Random(seed) stream, (pool_size,120) int8 piece types per pid. */
 int jq_generate_pool(int64_t seed, int32_t pool_size, int8_t *host_out);
+/* Canonical and mixed setup styles of GpuRollout (gpu_rollout.py:498-560).
+ * mode JQ_SETUP_CANONICAL: every seat takes the lineup of a style drawn with
+ * random.choice from `styles` (_build_canonical_pool, gpu_rollout.py:278-306);
+ * JQ_SETUP_MIXED: seats 0 and 2 take it, seats 1 and 3 draw uniform-random
+ * lineups in seat order (_build_mixed_pool, gpu_rollout.py:309-382). styles:
+ * nstyles letters of "TDGF" (CANONICAL_LINEUPS, setup_canonical.py:264-269)
+ * in the caller's order. per_game_seed != 0: setup i draws from
+ * random.Random(seed + i), as GpuRollout.reset (gpu_rollout.py:701-728); else
+ * all setups come from one random.Random(seed) stream, as the pool builders.
+ * host_out: (count, 120) int8 piece types per pid. Host only. */
+int jq_generate_styled(int32_t mode, int64_t seed, int32_t count, int32_t per_game_seed, const char *styles,
+                       int32_t nstyles, int8_t *host_out);
 /* Copy of the host-built constant board tables (struct jq::Tables of
  * junqi_amd/csrc/jq_topology.h), for inspection by tests. */
 int jq_board_tables(void *host_out, int64_t nbytes);

@@ -24,6 +24,7 @@ OBS_GLOBALS = 28
 AUX_PLANES = 6
 MAX_LEGAL = 3200
 SLOTS_PER_PIECE = 80
+SETUP_CANONICAL, SETUP_MIXED = 1, 2
 AUX_CHANNELS = (64, 65, 253, 254, 255, 256)
 
 FIELDS = {
@@ -39,7 +40,7 @@ FIELDS = {
 _EXPORTS = [
     "jq_last_error", "jq_version", "jq_create", "jq_destroy", "jq_num_envs", "jq_upload_zobrist",
     "jq_upload_recency", "jq_upload_setup_pool", "jq_reset_lineups", "jq_reset_seeded",
-    "jq_generate_lineups", "jq_generate_pool", "jq_board_tables", "jq_reset_terminated", "jq_step",
+    "jq_generate_lineups", "jq_generate_pool", "jq_generate_styled", "jq_board_tables", "jq_reset_terminated", "jq_step",
     "jq_legal", "jq_legal_slots", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_env_step",
     "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import", "jq_rehash",
     "jq_sync", "jq_history_create", "jq_history_destroy", "jq_history_bytes", "jq_history_snapshot",
@@ -70,7 +71,8 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_upload_zobrist": ([P, P, I64], C.c_int), "jq_upload_recency": ([P, P], C.c_int),
         "jq_upload_setup_pool": ([P, P, I32], C.c_int), "jq_reset_lineups": ([P, P, P], C.c_int),
         "jq_reset_seeded": ([P, I64, P], C.c_int), "jq_generate_lineups": ([I64, I32, P], C.c_int),
-        "jq_generate_pool": ([I64, I32, P], C.c_int), "jq_board_tables": ([P, I64], C.c_int),
+        "jq_generate_pool": ([I64, I32, P], C.c_int),
+        "jq_generate_styled": ([I32, I64, I32, I32, C.c_char_p, I32, P], C.c_int), "jq_board_tables": ([P, I64], C.c_int),
         "jq_reset_terminated": ([P, I64, P], C.c_int),
         "jq_step": ([P, P, P, I32, P, P, P, P, P, P, P, P, P, P], C.c_int),
         "jq_legal": ([P, P, P, P, P, P, P, P], C.c_int),

@@ -333,6 +333,22 @@ int jq_generate_pool(int64_t seed, int32_t pool_size, int8_t *host_out)
     return JQ_OK;
 }
 
+int jq_generate_styled(int32_t mode, int64_t seed, int32_t count, int32_t per_game_seed, const char *styles,
+                       int32_t nstyles, int8_t *host_out)
+{
+    if (mode != JQ_SETUP_CANONICAL && mode != JQ_SETUP_MIXED) return fail(JQ_E_ARG, "bad setup mode %d", mode);
+    if (!host_out || count < 0) return fail(JQ_E_ARG, "bad setup buffer");
+    if (!styles || nstyles <= 0) return fail(JQ_E_ARG, "setup styles must be non-empty");
+    std::vector<int8_t> idx((size_t)nstyles);
+    for (int32_t k = 0; k < nstyles; ++k) {
+        const int v = canonical_style(styles[k]);
+        if (v < 0) return fail(JQ_E_ARG, "unknown setup style '%c' (valid: D, F, G, T)", styles[k]);
+        idx[(size_t)k] = (int8_t)v;
+    }
+    generate_styled(mode, (uint64_t)seed, count, per_game_seed != 0, idx.data(), nstyles, host_out);
+    return JQ_OK;
+}
+
 int jq_board_tables(void *host_out, int64_t nbytes)
 {
     std::lock_guard<std::mutex> lk(g_tab_mu);

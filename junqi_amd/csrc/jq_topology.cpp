@@ -303,7 +303,52 @@ void lineup(MT &rng, int8_t *out)
     for (size_t k = 0; k < rest.size(); ++k) kind[rest[k]] = pieces[k];
     std::memcpy(out, kind, 30);
 }
+// The four canonical opening lineups T, D, G, F in seat-local slots (piece
+// types, 0 in the camps), as junqi_core/setup_canonical.py:96-269 defines them.
+const int8_t kCanonical[4][30] = {
+    {11, 13, 11, 13, 12, 12, 0, 13, 0, 12, 10, 4, 0, 11, 10, 7, 0, 9, 0, 7, 9, 8, 6, 8, 4, 3, 2, 5, 3, 3},
+    {13, 11, 13, 11, 13, 12, 0, 12, 0, 12, 10, 11, 0, 10, 4, 7, 0, 9, 0, 8, 8, 9, 7, 6, 4, 5, 2, 3, 3, 3},
+    {12, 11, 13, 11, 12, 12, 0, 13, 0, 13, 11, 10, 0, 10, 7, 9, 0, 7, 0, 9, 8, 4, 6, 4, 8, 3, 2, 3, 5, 3},
+    {13, 11, 11, 11, 13, 12, 0, 13, 0, 12, 10, 7, 0, 7, 10, 6, 0, 5, 0, 12, 9, 8, 4, 8, 9, 3, 2, 3, 4, 3},
+};
+
+// One styled setup: a style by random.choice, then per seat either that
+// style's lineup or (mixed, seats 1 and 3) a uniform-random lineup, in seat
+// order (gpu_rollout.py:296-305, 360-381).
+void styled_setup(MT &rng, int mode, const int8_t *styles, int nstyles, int8_t *out)
+{
+    const int st = styles[rng.below((uint32_t)nstyles)];
+    for (int s = 0; s < 4; ++s) {
+        if (mode == SETUP_MIXED && (s & 1)) lineup(rng, out + 30 * s);
+        else std::memcpy(out + 30 * s, kCanonical[st], 30);
+    }
+}
 }  // namespace
+
+int canonical_style(char c)
+{
+    switch (c) {
+    case 'T': return 0;
+    case 'D': return 1;
+    case 'G': return 2;
+    case 'F': return 3;
+    default: return -1;
+    }
+}
+
+void generate_styled(int mode, uint64_t seed, int count, bool per_game_seed, const int8_t *styles, int nstyles,
+                     int8_t *out)
+{
+    MT shared(seed);
+    for (int i = 0; i < count; ++i) {
+        if (per_game_seed) {
+            MT rng(seed + (uint64_t)i);
+            styled_setup(rng, mode, styles, nstyles, out + (size_t)i * 120);
+        } else {
+            styled_setup(shared, mode, styles, nstyles, out + (size_t)i * 120);
+        }
+    }
+}
 
 void generate_setup(uint64_t seed, int8_t out[120])
 {

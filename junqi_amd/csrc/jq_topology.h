@@ -66,4 +66,14 @@ void generate_setup(uint64_t seed, int8_t out[120]);
 // pool_size setups from one random.Random(seed) stream (junqi_rl/gpu_rollout.py:255-275)
 void generate_pool(uint64_t seed, int pool_size, int8_t *out);
 
+// Canonical / mixed setup styles of junqi_rl/gpu_rollout.py:278-382 and 701-728.
+enum { SETUP_CANONICAL = 1, SETUP_MIXED = 2 };
+// style letter 'T', 'D', 'G', 'F' -> index into the canonical lineups, else -1
+int canonical_style(char c);
+// count setups; styles are canonical_style indices. per_game_seed: setup i from
+// random.Random(seed + i) (GpuRollout.reset); else all from one random.Random(seed)
+// stream (the pool builders).
+void generate_styled(int mode, uint64_t seed, int count, bool per_game_seed, const int8_t *styles, int nstyles,
+                     int8_t *out);
+
 }  // namespace jq

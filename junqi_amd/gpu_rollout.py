@@ -20,6 +20,7 @@ import torch
 from . import _lib as L
 from .batch import JunqiBatch, generate_pool
 from .history import GpuRolloutHistory
+from .setups import _check_styles, arrangements_to_pool, generate_styled, lineups_to_vocab
 
 DEFAULT_POOL_SIZE = 10000
 OBS_CHANNELS = L.OBS_CHANNELS
@@ -45,17 +46,30 @@ class GpuRollout:
             raise ValueError(f"num_envs must be positive, got {num_envs}")
         if not torch.cuda.is_available() or torch.cuda.device_count() == 0:
             raise RuntimeError("No GPU found")
-        if canonical_setup_styles or mixed_setup:
-            raise NotImplementedError(
-                "canonical / mixed setup pools (junqi_core/setup_canonical.py) are not part of this build; "
-                "upload such a pool with upload_setup_pool() instead")
+        self._canonical_setup_styles = canonical_setup_styles
+        self._mixed_setup = bool(mixed_setup)
+        self._mixed_own_team_styles = tuple(mixed_own_team_styles)
+        if self._mixed_setup and not self._mixed_own_team_styles:
+            raise ValueError("mixed_setup=True requires mixed_own_team_styles to be non-empty")
+        # setup mode by precedence mixed > canonical > uniform (gpu_rollout.py:560-651)
+        if self._mixed_setup:
+            self._setup_mode = ("mixed", _check_styles(self._mixed_own_team_styles, "mixed_own_team_styles"))
+        elif canonical_setup_styles:
+            self._setup_mode = ("canonical", _check_styles(canonical_setup_styles, "canonical setup styles"))
+        else:
+            self._setup_mode = None
         move_limit = 4000 if max_num_moves is None else max_num_moves
         if move_limit <= 0:
             raise ValueError("max_num_moves must be positive")
         self.num_envs = int(num_envs)
         self.show_mode = show_mode
         self._device_id = int(device_id)
-        self._training_pool = generate_pool(42, DEFAULT_POOL_SIZE)
+        if self._setup_mode is None:
+            self._training_pool = generate_pool(42, DEFAULT_POOL_SIZE)
+        else:
+            self._training_pool = generate_styled(self._setup_mode[0], 42, DEFAULT_POOL_SIZE, self._setup_mode[1],
+                                                  per_game_seed=False)
+        self.last_setup_pool_unique = 0
         self._b = JunqiBatch(self.num_envs, show_mode=_show_value(show_mode), max_num_moves=move_limit,
                              device=self._device_id, setup_pool=self._training_pool)
         dev = self._b.device
@@ -90,11 +104,31 @@ class GpuRollout:
             return 0
         return self.upload_setup_pool(self._training_pool)
 
+    def refresh_setup_pool_from_arrangements(self, samples: torch.Tensor, seat_idx: torch.Tensor, *,
+                                             pool_size: int = 0, seed: int = 0) -> int:
+        """Install a pool built from arrangement-net samples as the training pool
+        (gpu_rollout.py:1034-1081): (n_arr, 30, 13) one-hot samples and their
+        (n_arr,) seats, zip or independent pairing. Returns the pool size."""
+        pool = arrangements_to_pool(samples, seat_idx, pool_size=int(pool_size), seed=int(seed))
+        self.upload_setup_pool(pool)
+        self._training_pool = pool
+        self.last_setup_pool_unique = int(np.unique(pool, axis=0).shape[0])
+        return int(pool.shape[0])
+
+    def snapshot_env_arrangements(self) -> np.ndarray:
+        """(N, 4, 30) int64 vocabulary indices of each env's lineup
+        (gpu_rollout.py:1083-1100)."""
+        return lineups_to_vocab(self._b.get_field("ptype")[:, :120])
+
     # ------------------------------------------------------------ lifecycle
     def reset(self, seed_base: int = 0) -> None:
-        """Fresh games: env i gets generate_random_setup(random.Random(seed_base + i))
-        (gpu_rollout.py:690-744)."""
-        self._b.reset(int(seed_base))
+        """Fresh games from random.Random(seed_base + i) per env: uniform-random
+        setups, or the canonical / mixed style draw (gpu_rollout.py:690-744)."""
+        if self._setup_mode is None:
+            self._b.reset(int(seed_base))
+        else:
+            mode, styles = self._setup_mode
+            self._b.reset_lineups(generate_styled(mode, int(seed_base), self.num_envs, styles, per_game_seed=True))
         self._last_result = None
 
     def reset_from_setup_pool(self, seed: int = 0) -> None:

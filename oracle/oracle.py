@@ -78,6 +78,7 @@ def lib() -> C.CDLL:
     L.jqo_random_lineup.argtypes = [P, P]
     L.jqo_random_setup.argtypes = [C.c_uint64, P]
     L.jqo_setup_pool.argtypes = [C.c_uint64, C.c_int32, P]
+    L.jqo_random_lineup.argtypes = [P, P]
     L.jqo_seedseq_state.argtypes = [C.c_uint64, P]
     L.jqo_pcg64_draw.argtypes = [C.c_uint64, C.c_int64, P]
     L.jqo_zobrist_count.restype = C.c_int64
@@ -157,6 +158,29 @@ class MT:
 
     def choice(self, seq):
         return seq[self.randbelow(len(seq))]
+
+    def random_lineup(self) -> np.ndarray:
+        """generate_random_lineup(rng) (junqi_core/setup.py:162-250) on this stream."""
+        out = np.zeros(30, dtype=np.int8)
+        lib().jqo_random_lineup(_p(self._buf), _p(out))
+        return out
+
+
+def styled_setups(mode: str, seed: int, count: int, styles, lineups: dict, *, per_game_seed: bool) -> np.ndarray:
+    """Canonical / mixed setups (junqi_rl/gpu_rollout.py:278-382 pools from one
+    random.Random(seed) stream; :701-728 reset with random.Random(seed + i) per
+    game). `lineups` maps a style letter to its 30 seat-local types."""
+    out = np.zeros((count, 120), dtype=np.int8)
+    shared = MT(seed)
+    for i in range(count):
+        rng = MT(seed + i) if per_game_seed else shared
+        own = np.asarray(lineups[rng.choice(list(styles))], dtype=np.int8)
+        for s in range(4):
+            if mode == "mixed" and s in (1, 3):
+                out[i, 30 * s:30 * s + 30] = rng.random_lineup()
+            else:
+                out[i, 30 * s:30 * s + 30] = own
+    return out
 
 
 class Game:

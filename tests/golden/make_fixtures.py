@@ -1,8 +1,9 @@
 """Write the committed fixtures under tests/golden/ (run once, in the build container).
 
 It reads only DATA files of the reference repository (JSON scenarios, the
-recorded game) and calls numpy / the standard library. It imports no
-reference code. Usage::
+recorded game), parses the canonical lineup tables out of
+junqi_core/setup_canonical.py as text (``ast``; nothing is executed) and calls
+numpy / the standard library. It imports no reference code. Usage::
 
     python tests/golden/make_fixtures.py [/path/to/reference]
 
@@ -18,10 +19,13 @@ recency_lut_f32.bin                float32 exp(-e/tau) for e in [0,4096) (also w
                                    tau planes (32, 256, 64, 128), computed the way
                                    junqi_core/observation.py:1561-1562 does
 zobrist_sha256.txt                 SHA-256 of the numpy PCG64 Zobrist stream
+canonical_lineups.json             the four canonical opening lineups T, D, G, F as
+                                   30 seat-local piece types (setup_canonical.py:96-269)
 """
 
 from __future__ import annotations
 
+import ast
 import hashlib
 import json
 import shutil
@@ -91,6 +95,29 @@ def replay(ref: Path) -> dict:
     return {"lineups": lineups, "jql_moves": moves, "plies": plies}
 
 
+def canonical_lineups(ref: Path) -> dict:
+    """SETUP_<style> = _make_lineup({slot: PieceType.NAME, ...}) literals of
+    setup_canonical.py, read from its syntax tree."""
+    tree = ast.parse((ref / "junqi_core" / "setup_canonical.py").read_text())
+    out = {}
+    for node in ast.walk(tree):
+        if not isinstance(node, (ast.Assign, ast.AnnAssign)):
+            continue
+        target = node.targets[0] if isinstance(node, ast.Assign) else node.target
+        if not (isinstance(target, ast.Name) and target.id.startswith("SETUP_")):
+            continue
+        call = node.value
+        assert isinstance(call, ast.Call) and call.func.id == "_make_lineup", target.id
+        table = call.args[0]
+        row = [0] * 30
+        for k, v in zip(table.keys, table.values):
+            assert isinstance(v, ast.Attribute) and v.value.id == "PieceType", target.id
+            row[k.value] = TYPE_NAMES.index(v.attr)
+        out[target.id[len("SETUP_"):]] = row
+    assert sorted(out) == ["D", "F", "G", "T"], sorted(out)
+    return out
+
+
 def main() -> None:
     ref = Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
     for cat in CATEGORIES:
@@ -106,6 +133,7 @@ def main() -> None:
     z = zobrist_stream()
     (HERE / "zobrist_sha256.txt").write_text(
         f"{hashlib.sha256(z.astype('<u8').tobytes()).hexdigest()}  {z.size} uint64 (little-endian)\n")
+    (HERE / "canonical_lineups.json").write_text(json.dumps(canonical_lineups(ref)) + "\n")
     print("fixtures written to", HERE)
 
 

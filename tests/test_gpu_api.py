@@ -295,3 +295,66 @@ def test_uploaded_beliefs_feed_the_observation(jq):
             assert np.array_equal(wsp[i, k][planes], g.observe(k, bel[i, k])[0][planes]), (i, k)
             assert np.array_equal(wsp[i, k][other], wsp0[i, k][other]), (i, k)
     w.state.close()
+
+
+def test_setup_styles_and_arrangement_pools(jq):
+    """Canonical / mixed setup styles and arrangement pools
+    (gpu_rollout.py:498-744,1034-1100; tests/test_gpu_rollout.py:165-207)."""
+    import json
+
+    from tests import helpers as H
+
+    lu = json.loads((H.GOLDEN / "canonical_lineups.json").read_text())
+    n = 16
+    print("[styles] canonical reset", flush=True)
+    ro = jq.GpuRollout(n, canonical_setup_styles=("T", "D"))
+    ro.reset(seed_base=5)
+    want = O.styled_setups("canonical", 5, n, ("T", "D"), lu, per_game_seed=True)
+    games = [O.Game(w, show_mode=1) for w in want]
+    G.compare_state(G.device_fields(ro.batch), G.oracle_fields(games), ctx="canonical reset")
+    ro.close()
+    with pytest.raises(ValueError, match="unknown canonical setup styles"):
+        jq.GpuRollout(2, canonical_setup_styles=("Q",))
+    with pytest.raises(ValueError, match="non-empty"):
+        jq.GpuRollout(2, mixed_setup=True, mixed_own_team_styles=())
+
+    print("[styles] mixed pool through evaluation", flush=True)
+    ro = jq.GpuRollout(n, mixed_setup=True, mixed_own_team_styles=("T",))
+    ro.reset(seed_base=0)
+    want = O.styled_setups("mixed", 0, n, ("T",), lu, per_game_seed=True)
+    assert np.array_equal(ro.batch.get_field("ptype")[:, :120].reshape(n, 120).clip(0), want.clip(0))
+
+    def own_lineups() -> set:
+        pt = ro.batch.get_field("ptype")[:, :120].reshape(n, 4, 30).clip(0)   # camps hold -1 on device
+        return {tuple(int(v) for v in r) for r in pt[:, 0, :]}
+
+    def restart(seed: int) -> None:
+        ro.batch.set_field("terminated", np.ones(n, np.uint8))
+        ro.reset_terminated_device(seed=seed)
+
+    restart(1)
+    assert own_lineups() == {tuple(lu["T"])}
+    ro.upload_fixed_evaluation_setup_pool(seed=20_260_817)
+    restart(2)
+    assert len(own_lineups()) > 1
+    assert ro.restore_training_setup_pool() > 0
+    restart(3)
+    assert own_lineups() == {tuple(lu["T"])}
+
+    print("[styles] arrangement pool refresh", flush=True)
+    base = O.setup_pool(11, 8)
+    from junqi_amd.setups import lineups_to_vocab
+    vocab = torch.from_numpy(lineups_to_vocab(base).reshape(32, 30))
+    samples = torch.nn.functional.one_hot(vocab, 13).float()
+    seat_idx = torch.arange(4).repeat(8)
+    assert ro.refresh_setup_pool_from_arrangements(samples, seat_idx) == 8
+    assert ro.last_setup_pool_unique == len({tuple(r) for r in base})
+    ro.reset_from_setup_pool(seed=4)
+    pool = ro.batch.pool
+    assert np.array_equal(pool, base)
+    games = [O.Game(pool[G.reset_pool_index(i, 4, pool.shape[0])], show_mode=1) for i in range(n)]
+    G.compare_state(G.device_fields(ro.batch), G.oracle_fields(games), ctx="arrangement pool reset")
+    arr = ro.snapshot_env_arrangements()
+    assert arr.shape == (n, 4, 30) and arr.dtype == np.int64
+    assert np.array_equal(arr, lineups_to_vocab(np.stack([g.buf[0]["ptype"] for g in games])))
+    ro.close()

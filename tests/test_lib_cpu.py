@@ -239,3 +239,69 @@ def test_mask_helpers_validate_without_gpu():
     with pytest.raises(ValueError, match="CUDA"):
         csr_to_dense_selected(torch.zeros((4, 8), dtype=torch.int32), torch.zeros(4, dtype=torch.int32),
                               torch.zeros(2, dtype=torch.int64), 16641)
+
+
+@pytest.mark.parametrize("mode", ["canonical", "mixed"])
+@pytest.mark.parametrize("styles", [("T",), ("T", "D", "G", "F"), ("F", "F", "G")])
+def test_styled_setups_match_oracle(jl, mode, styles):
+    """jq_generate_styled (host code of the library) equals the oracle's
+    restatement of the canonical / mixed pool builders and per-game resets,
+    with the lineups taken from the fixture parsed out of setup_canonical.py."""
+    import json
+
+    from junqi_amd.setups import canonical_lineup, generate_styled
+    from tests import helpers as H
+
+    lu = json.loads((H.GOLDEN / "canonical_lineups.json").read_text())
+    for k in "TDGF":
+        assert np.array_equal(canonical_lineup(k), np.asarray(lu[k], np.int8))
+    for per_game in (False, True):
+        got = generate_styled(mode, 42, 64, styles, per_game_seed=per_game)
+        want = O.styled_setups(mode, 42, 64, styles, lu, per_game_seed=per_game)
+        assert np.array_equal(got, want), (mode, styles, per_game)
+
+
+def test_styled_setup_errors(jl):
+    from junqi_amd.setups import generate_styled
+
+    with pytest.raises(ValueError, match="unknown setup styles"):
+        generate_styled("canonical", 0, 4, ("T", "X"), per_game_seed=False)
+    with pytest.raises(ValueError, match="non-empty"):
+        generate_styled("mixed", 0, 4, (), per_game_seed=False)
+    out = np.zeros((1, 120), np.int8)
+    assert jl.lib.jq_generate_styled(7, 0, 1, 0, b"T", 1, out.ctypes.data) != 0
+    assert b"bad setup mode" in jl.lib.jq_last_error()
+    assert jl.lib.jq_generate_styled(1, 0, 1, 0, b"Q", 1, out.ctypes.data) != 0
+    assert b"unknown setup style" in jl.lib.jq_last_error()
+
+
+def test_arrangement_pools():
+    """arrangements_to_pool (pool_upload.py:62-150): zip pairing keeps the k-th
+    sample of every seat, independent pairing keeps that prefix and draws the
+    tail per seat from that seat's samples; vocabulary indices round-trip."""
+    import torch
+
+    from junqi_amd.setups import arrangements_to_pool, lineups_to_vocab
+
+    base = O.setup_pool(3, 12)                      # 12 setups -> 48 seat lineups
+    vocab = lineups_to_vocab(base)                  # (12, 4, 30)
+    assert vocab.max() <= 12 and vocab.min() >= 0
+    seats = np.tile(np.arange(4), 12)
+    order = np.random.default_rng(0).permutation(48)
+    samples = torch.nn.functional.one_hot(torch.from_numpy(vocab.reshape(48, 30)[order]), 13).float()
+    seat_idx = torch.from_numpy(seats[order])
+    zip_pool = arrangements_to_pool(samples, seat_idx)
+    assert zip_pool.shape == (12, 120)
+    for s in range(4):
+        rows = order[seats[order] == s]             # flat (setup*4 + seat) of seat s samples in order
+        assert np.array_equal(zip_pool[:, 30 * s:30 * s + 30], base.reshape(48, 30)[rows])
+    big = arrangements_to_pool(samples, seat_idx, pool_size=100, seed=7)
+    assert big.shape == (100, 120) and np.array_equal(big[:12], zip_pool)
+    assert np.array_equal(big, arrangements_to_pool(samples, seat_idx, pool_size=100, seed=7))
+    for s in range(4):
+        allowed = {tuple(r) for r in zip_pool[:, 30 * s:30 * s + 30]}
+        assert {tuple(r) for r in big[:, 30 * s:30 * s + 30]} <= allowed
+    with pytest.raises(ValueError, match="zero arrangement samples"):
+        arrangements_to_pool(samples[seat_idx != 2], seat_idx[seat_idx != 2])
+    with pytest.raises(ValueError, match="samples must be"):
+        arrangements_to_pool(samples[:, :29], seat_idx)

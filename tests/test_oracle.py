@@ -52,17 +52,61 @@ def test_seedsequence_other_seed():
     assert np.array_equal(got, ref)
 
 
+def _assert_c1_c5(lineup):
+    """validate_lineup (junqi_core/setup.py): camps empty, flag in a stronghold,
+    mines in the back two rows, bombs off the front row, piece counts."""
+    lineup = np.asarray(lineup)
+    counts = {2: 1, 3: 3, 4: 2, 5: 1, 6: 1, 7: 2, 8: 2, 9: 2, 10: 2, 11: 3, 12: 3, 13: 3}
+    assert all(lineup[i] == 0 for i in (6, 8, 12, 16, 18))
+    assert (lineup == 2).sum() == 1 and int(np.nonzero(lineup == 2)[0][0]) in (26, 28)
+    assert all(i >= 20 for i in np.nonzero(lineup == 3)[0])
+    assert all(i >= 5 for i in np.nonzero(lineup == 4)[0])
+    for t, c in counts.items():
+        assert (lineup == t).sum() == c
+
+
 @pytest.mark.parametrize("seed", range(40))
 def test_random_setup_satisfies_c1_c5(seed):
-    s = O.random_setup(seed).reshape(4, 30)
-    counts = {2: 1, 3: 3, 4: 2, 5: 1, 6: 1, 7: 2, 8: 2, 9: 2, 10: 2, 11: 3, 12: 3, 13: 3}
-    for lineup in s:
-        assert all(lineup[i] == 0 for i in (6, 8, 12, 16, 18))
-        assert (lineup == 2).sum() == 1 and int(np.nonzero(lineup == 2)[0][0]) in (26, 28)
-        assert all(i >= 20 for i in np.nonzero(lineup == 3)[0])
-        assert all(i >= 5 for i in np.nonzero(lineup == 4)[0])
-        for t, c in counts.items():
-            assert (lineup == t).sum() == c
+    for lineup in O.random_setup(seed).reshape(4, 30):
+        _assert_c1_c5(lineup)
+
+
+def test_canonical_lineup_fixture():
+    """The canonical lineups parsed from setup_canonical.py pass the module's
+    own self-test (C1-C5, setup_canonical.py:317-333) and its stated layouts:
+    flag at 26 in all four, SILING at 27 (T), 25 (D), 28 (G), 17 (F)."""
+    lu = json.loads((H.GOLDEN / "canonical_lineups.json").read_text())
+    assert sorted(lu) == ["D", "F", "G", "T"]
+    for style, row in lu.items():
+        _assert_c1_c5(row)
+        assert row[26] == 2
+    assert [lu[k].index(5) for k in "TDGF"] == [27, 25, 28, 17]
+
+
+@pytest.mark.parametrize("mode", ["canonical", "mixed"])
+def test_styled_setups_oracle(mode):
+    """Styled pools draw the style with random.choice and, in mixed mode, the
+    two enemy seats' random lineups from the same stream in seat order: with a
+    single style the draws only advance the stream, so the enemy seats equal
+    the random lineups of a stream advanced by one choice."""
+    lu = json.loads((H.GOLDEN / "canonical_lineups.json").read_text())
+    out = O.styled_setups(mode, 5, 6, ("G",), lu, per_game_seed=False)
+    rng = O.MT(5)
+    for i in range(6):
+        assert rng.choice(["G"]) == "G"
+        for s in range(4):
+            if mode == "mixed" and s in (1, 3):
+                want = rng.random_lineup()
+                _assert_c1_c5(want)
+            else:
+                want = np.asarray(lu["G"], np.int8)
+            assert np.array_equal(out[i, 30 * s:30 * s + 30], want)
+    per = O.styled_setups(mode, 9, 3, ("T", "D", "F"), lu, per_game_seed=True)
+    for i in range(3):
+        one = O.styled_setups(mode, 9 + i, 1, ("T", "D", "F"), lu, per_game_seed=False)
+        assert np.array_equal(per[i], one[0])
+    styles = {tuple(r[:30]) for r in O.styled_setups(mode, 1, 200, ("T", "D", "F"), lu, per_game_seed=False)}
+    assert styles == {tuple(lu[k]) for k in "TDF"}
 
 
 # ---------------------------------------------------------------- topology
