@@ -675,10 +675,9 @@ __device__ __forceinline__ void obs_emit_aux(const ObsLds &L, float *row, int ct
     if (ct == 192) for (int e = ql * 4 - lead; e < AUX_ROW; ++e) row[e] = aux_at(L, e);
 }
 
-// u8 row emission: the row's full 16-byte chunks are split into contiguous
-// ranges, one per wave; a lane writes two chunks per iteration (the wave covers
-// 2 KB), so two independent LDS -> expand -> store chains overlap. The aux
-// planes follow, spread over the block.
+// u8 row emission: the row's full 16-byte chunks, in 1 KB units of the output
+// buffer split into contiguous runs, one per wave. The aux planes follow,
+// spread over the block.
 __device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m, float *aux, int ct)
 {
     const int lead = m;
@@ -688,16 +687,25 @@ __device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m
     const int wv = __builtin_amdgcn_readfirstlane(ct >> 6);
     const int lane = ct & 63;
     constexpr int NW = OBS_THREADS / 64;
-    const int nq = ql - qf;
-    const int fair = (nq + NW - 1) / NW;
-    const int per = ((fair + 64) / 128) * 128;                  // whole 2 KB steps, nearest to fair
-    const int wa = min(ql, qf + wv * per), wb = wv == NW - 1 ? ql : min(ql, wa + per);
     // chunk q covers row bytes [q*16 - m, q*16 - m + 16): a 16-byte aligned slot
     // of the output, indexed from the aligned address below the row start
     uint4 *__restrict__ slot = reinterpret_cast<uint4 *>(__builtin_assume_aligned(row - m, 16));
-    for (int q = wa + lane; q < wb; q += 64) {
-        const int e0 = q * 16 - m;
-        slot[q] = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
+    // Each wave iteration stores one whole, 1 KB-aligned unit of the buffer (the
+    // row's first and last units in part), and each wave owns a contiguous run
+    // of units: a 128-byte line is never split between two store instructions.
+    const uint64_t gbase = (uint64_t)(uintptr_t)(row - m) >> 4;   // buffer slot of chunk 0
+    const uint64_t gA = gbase + qf, gB = gbase + ql;
+    const uint64_t u0 = gA >> 6, u1 = (gB + 63) >> 6;
+    const int nu = (int)(u1 - u0);
+    const int per = (nu + NW - 1) / NW;
+    const int ka = min(nu, wv * per), kb = min(nu, ka + per);
+    for (int k = ka; k < kb; ++k) {
+        const uint64_t g = ((u0 + k) << 6) + lane;
+        if (g >= gA && g < gB) {
+            const int q = (int)(g - gbase);
+            const int e0 = q * 16 - m;
+            slot[q] = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
+        }
     }
     // partial chunks at the two ends of the row
     if (ct == 0 && lead) obs_elems<2>(L, row, 0, 16 - m, m);
