@@ -619,14 +619,21 @@ __device__ __forceinline__ void belief_update(const State &S, int env, const int
     S.env[env].remtrk[o] = trk;
 }
 
-__global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict__ actions,
-                                             const int8_t *__restrict__ acting, int act_fmt, StepOut O)
+// What the env record says after a step (wave-uniform), for work that follows
+// the step in the same kernel.
+struct TurnAfter {
+    int turn;
+    bool term;
+    uint8_t sdead;
+};
+
+// One ply of env `env` by its wave (GameState.step_inplace, state.py:700-1167).
+// cell / pos / ptype are the wave's LDS arrays; on return they hold the board
+// after the step (unchanged if the action was not applied).
+__device__ void step_env(const State &S, int env, int l, const int32_t *__restrict__ actions,
+                         const int8_t *__restrict__ acting, int act_fmt, const StepOut &O, int8_t *cell, int16_t *pos,
+                         int8_t *ptype, TurnAfter &nx)
 {
-    const int env = blockIdx.x, l = threadIdx.x;
-    if (env >= S.n) return;
-    __shared__ int8_t cell[CELL_STRIDE];
-    __shared__ int16_t pos[PID_STRIDE];
-    __shared__ int8_t ptype[PID_STRIDE];
 
     // the board, the piece records, the env record and the action are all
     // loaded into registers first (one memory round trip), then staged in LDS;
@@ -647,6 +654,7 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     pos[l + 64] = r1.pos; ptype[l + 64] = r1.ptype;
     const bool was_term = E.term != 0;
     const int seat = E.turn;
+    nx.turn = seat; nx.term = was_term; nx.sdead = E.sdead;
     if (l == 0) {
         if (O.valid) O.valid[env] = 0;
         if (O.event) O.event[env] = 0;
@@ -772,6 +780,7 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
 
     belief_update(S, env, cell, sp, dp, ss, ds, dt, dst, ev, rsrc, rdst, fcap, died);
 
+    nx.turn = nturn; nx.term = term != 0; nx.sdead = sdead;
     if (l == 0) {
         EnvRec &W = S.env[env];   // remtrk belongs to belief_update's lanes
         W.zob = zob; W.mc = nmc; W.mslc = nmslc;
@@ -787,6 +796,18 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
         if (O.died) O.died[env] = (uint8_t)died;
         if (O.reward) O.reward[env] = (term && !drw && win >= 0) ? (((seat & 1) == win) ? 1.f : -1.f) : 0.f;
     }
+}
+
+__global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict__ actions,
+                                             const int8_t *__restrict__ acting, int act_fmt, StepOut O)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    __shared__ int8_t cell[CELL_STRIDE];
+    __shared__ int16_t pos[PID_STRIDE];
+    __shared__ int8_t ptype[PID_STRIDE];
+    TurnAfter nx;
+    step_env(S, env, l, actions, acting, act_fmt, O, cell, pos, ptype, nx);
 }
 
 // ------------------------------------------------------------------ reset
@@ -829,12 +850,18 @@ __global__ __launch_bounds__(64) void k_clear(State S)
 }
 
 // Start an env from a lineup (GameState.new_game, state.py:490-620; beliefs,
-// info_model.py:218-265). Zobrist includes every term new_game XORs in.
-__device__ void init_env(const State &S, int env, const int8_t *types)
+// info_model.py:218-265). Zobrist includes every term new_game XORs in. If
+// lcell is given, the new board is also staged in the wave's LDS arrays
+// lcell / lpos / ltype (as step_env leaves them).
+__device__ void init_env(const State &S, int env, const int8_t *types, int8_t *lcell = nullptr,
+                         int16_t *lpos = nullptr, int8_t *ltype = nullptr)
 {
     const int l = lane_id();
     int8_t *cell = S.cell + (size_t)env * CELL_STRIDE;
-    for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = -1;
+    for (int f = l; f < CELL_STRIDE; f += 64) {
+        cell[f] = -1;
+        if (lcell) lcell[f] = -1;
+    }
     __syncthreads();
     uint64_t z = 0;
     for (int p = l; p < PID_STRIDE; p += 64) {
@@ -849,6 +876,11 @@ __device__ void init_env(const State &S, int env, const int8_t *types)
         r.dreason = -1; r.dstep = -1; r.dloc = -1;
         S.piece[pi] = r;
         if (alive) { cell[h] = (int8_t)p; z ^= zp(S.ztab, p, t, h); }
+        if (lcell) {
+            if (alive) lcell[h] = (int8_t)p;
+            lpos[p] = (int16_t)h;
+            ltype[p] = r.ptype;
+        }
         for (int o = 0; o < 4; ++o) {
             uint8_t code = 0;
             if (alive) code = sees_truth(o, p / 30, S.show_mode) ? (uint8_t)(1 + t - 2) : (uint8_t)(BC_PRIOR0 + p % 30);
@@ -886,17 +918,22 @@ __global__ __launch_bounds__(64) void k_reset_lineups(State S, const int8_t *__r
     init_env(S, env, lineups + (size_t)env * NP);
 }
 
-__global__ __launch_bounds__(64) void k_reset_terminated(State S, int64_t seed)
+// Pool entry a finished env restarts from: the reference reset kernel's hash
+// (game_state.cu:2986-2991).
+__device__ __forceinline__ int reset_pool_index(int env, int64_t seed, int pool_size)
 {
-    const int env = blockIdx.x;
-    if (env >= S.n || !S.env[env].term) return;
-    // pool pick of the reference reset kernel (game_state.cu:2986-2991)
     uint64_t h = (uint64_t)env * 2654435761ull + (uint64_t)seed;
     h ^= h >> 17;
     h *= 0xbf58476d1ce4e5b9ull;
     h ^= h >> 31;
-    const int idx = (int)(h % (uint64_t)S.pool_size);
-    init_env(S, env, S.pool + (size_t)idx * NP);
+    return (int)(h % (uint64_t)pool_size);
+}
+
+__global__ __launch_bounds__(64) void k_reset_terminated(State S, int64_t seed)
+{
+    const int env = blockIdx.x;
+    if (env >= S.n || !S.env[env].term) return;
+    init_env(S, env, S.pool + (size_t)reset_pool_index(env, seed, S.pool_size) * NP);
 }
 
 // Recompute Zobrist and (if `beliefs`) re-seed beliefs from the current board
@@ -954,25 +991,14 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
 // Per env: masks of the acting seat's movable pieces (lanes = pieces), engineer
 // closures, counts, the packed canonical mask and the CSR scratch in ascending
 // source order (move_gen.py:1199 sorts the ids).
-__global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict__ acting,
-                                              int32_t *__restrict__ counts, int32_t *__restrict__ mask_words,
-                                              uint8_t *__restrict__ mask_bool)
+// Legal sets of env `env` for `seat` by its wave (off: none): the board in LDS
+// (cell, padded to CELL_STRIDE with -1), bits cleared and, for the canonical
+// mask, rotl filled. Piece positions / types come from the LDS arrays lpos /
+// ltype when given, else from the piece records.
+__device__ __forceinline__ void legal_body(const State &S, int env, int l, int seat, bool off, const int8_t *cell, uint32_t *bits,
+                           const uint8_t *rotl, const int16_t *lpos, const int8_t *ltype, int32_t *__restrict__ counts,
+                           int32_t *__restrict__ mask_words, uint8_t *__restrict__ mask_bool)
 {
-    const int env = blockIdx.x, l = threadIdx.x;
-    if (env >= S.n) return;
-    __shared__ int8_t cell[CELL_STRIDE];
-    __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
-    __shared__ uint8_t rotl[NONB + 3];   // world compact -> canonical compact of the acting seat
-    const EnvRec &E = S.env[env];
-    const int seat = acting ? acting[env] : E.turn;
-    const bool off = E.term || seat < 0 || seat > 3 || ((E.sdead >> (seat & 3)) & 1);
-    for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
-    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
-    if (mask_words || mask_bool) {
-        const int s4 = seat & 3;
-        for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[s4][c];
-    }
-    __syncthreads();
     const int team = seat & 1;
     BB occ, ea;
     env_boards(cell, team, occ, ea);
@@ -983,9 +1009,15 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     uint64_t m0 = 0, m1 = 0, m2 = 0;
     if (!off && p < 30) {
         const int pid = seat * 30 + p;
-        const PieceRec r = S.piece[pc_idx(env, pid)];
-        src = r.pos;
-        const int t = r.ptype;
+        int t;
+        if (lpos) {
+            src = lpos[pid];
+            t = ltype[pid];
+        } else {
+            const PieceRec r = S.piece[pc_idx(env, pid)];
+            src = r.pos;
+            t = r.ptype;
+        }
         mov = (unsigned)src < (unsigned)NC && t != T_JUNQI && t != T_DILEI && !flat_has(cT.shm, src);
         if (mov) {
             eng = t == T_GONGB;
@@ -1076,7 +1108,60 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
             *reinterpret_cast<uint4 *>(row + i0) = make_uint4(v[0], v[1], v[2], v[3]);
         }
         for (int i = head + nchunks * 16 + l; i < JQ_ACTION_DIM; i += 64) row[i] = (bits[i >> 5] >> (i & 31)) & 1;
+    }}
+
+__global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict__ acting,
+                                              int32_t *__restrict__ counts, int32_t *__restrict__ mask_words,
+                                              uint8_t *__restrict__ mask_bool)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    __shared__ int8_t cell[CELL_STRIDE];
+    __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
+    __shared__ uint8_t rotl[NONB + 3];   // world compact -> canonical compact of the acting seat
+    const EnvRec &E = S.env[env];
+    const int seat = acting ? acting[env] : E.turn;
+    const bool off = E.term || seat < 0 || seat > 3 || ((E.sdead >> (seat & 3)) & 1);
+    for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
+    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
+    if (mask_words || mask_bool) {
+        const int s4 = seat & 3;
+        for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[s4][c];
     }
+    __syncthreads();
+    legal_body(S, env, l, seat, off, cell, bits, rotl, nullptr, nullptr, counts, mask_words, mask_bool);
+}
+
+// One env-step's state work by one wave per env: the ply (k_step), the restart
+// of a finished game from the setup pool (k_reset_terminated, if do_reset) and
+// the legal sets of the next acting seat (k_legal with the current
+// turn), on the board the wave keeps in LDS, with no global round trip between
+// the three.
+__global__ __launch_bounds__(64) void k_env_step(State S, const int32_t *__restrict__ actions, StepOut O,
+                                                 int do_reset, int64_t reset_seed, int32_t *__restrict__ counts,
+                                                 int32_t *__restrict__ mask_words)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    __shared__ int8_t cell[CELL_STRIDE];
+    __shared__ int16_t pos[PID_STRIDE];
+    __shared__ int8_t ptype[PID_STRIDE];
+    __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
+    __shared__ uint8_t rotl[NONB + 3];
+    TurnAfter nx;
+    step_env(S, env, l, actions, nullptr, 0, O, cell, pos, ptype, nx);
+    __syncthreads();
+    if (do_reset && S.pool_size > 0 && nx.term) {
+        init_env(S, env, S.pool + (size_t)reset_pool_index(env, reset_seed, S.pool_size) * NP, cell, pos, ptype);
+        nx.turn = 0; nx.term = false; nx.sdead = 0;
+    }
+    const int seat = nx.turn;
+    const bool off = nx.term || seat < 0 || seat > 3 || ((nx.sdead >> (seat & 3)) & 1);
+    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
+    if (mask_words)
+        for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[seat & 3][c];
+    __syncthreads();
+    legal_body(S, env, l, seat, off, cell, bits, rotl, pos, ptype, counts, mask_words, nullptr);
 }
 
 // Exclusive scan of counts into offsets (N+1); one 1024-thread block walks the

@@ -529,13 +529,20 @@ int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_
         if ((rc = jq_sample_uniform(e, counts, offsets, values, sample_seed, ply, dst, stream)) != 0) return rc;
         act = dst;
     }
-    if ((rc = jq_step(e, act, nullptr, JQ_ACT_WORLD, nullptr, nullptr, terminated, nullptr, nullptr, nullptr,
-                      nullptr, reward, nullptr, stream)) != 0)
-        return rc;
-    if (e->S.pool && (rc = jq_reset_terminated(e, reset_seed, stream)) != 0) return rc;
+    if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before stepping");
+    StepOut O = {};
+    O.term = terminated;
+    O.reward = reward;
+    // ply, restart from the pool and the next seat's legal sets in one kernel
+    hipLaunchKernelGGL(k_env_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, act, O, e->S.pool ? 1 : 0,
+                       reset_seed, counts, mask_words);
+    if ((rc = launch_check("k_env_step")) != 0) return rc;
+    hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, strm(stream), counts, offsets, e->S.n);
+    if ((rc = launch_check("k_scan")) != 0) return rc;
+    hipLaunchKernelGGL(k_emit, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, offsets, values);
+    if ((rc = launch_check("k_emit")) != 0) return rc;
     // sequential on purpose: the u8 observation grid holds every CU's LDS, so a
-    // concurrent legal-action launch only slows both down
-    if ((rc = jq_legal(e, nullptr, counts, offsets, values, mask_words, nullptr, stream)) != 0) return rc;
+    // concurrent launch only slows both down
     if (spatial && (rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream)) != 0) return rc;
     return JQ_OK;
 }
