@@ -630,9 +630,8 @@ struct TurnAfter {
 // One ply of env `env` by its wave (GameState.step_inplace, state.py:700-1167).
 // cell / pos / ptype are the wave's LDS arrays; on return they hold the board
 // after the step (unchanged if the action was not applied).
-__device__ void step_env(const State &S, int env, int l, const int32_t *__restrict__ actions,
-                         const int8_t *__restrict__ acting, int act_fmt, const StepOut &O, int8_t *cell, int16_t *pos,
-                         int8_t *ptype, TurnAfter &nx)
+__device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t *__restrict__ acting, int act_fmt,
+                         const StepOut &O, int8_t *cell, int16_t *pos, int8_t *ptype, TurnAfter &nx)
 {
 
     // the board, the piece records, the env record and the action are all
@@ -645,7 +644,6 @@ __device__ void step_env(const State &S, int env, int l, const int32_t *__restri
         cv[k] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : (int8_t)-1;
     }
     const PieceRec r0 = S.piece[pc_idx(env, l)], r1 = S.piece[pc_idx(env, l + 64)];
-    const int32_t a = actions[env];
     const EnvRec &E = S.env[env];   // uniform: scalar loads
 #pragma unroll
     for (int k = 0; k < 5; ++k)
@@ -807,7 +805,7 @@ __global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict_
     __shared__ int16_t pos[PID_STRIDE];
     __shared__ int8_t ptype[PID_STRIDE];
     TurnAfter nx;
-    step_env(S, env, l, actions, acting, act_fmt, O, cell, pos, ptype, nx);
+    step_env(S, env, l, actions[env], acting, act_fmt, O, cell, pos, ptype, nx);
 }
 
 // ------------------------------------------------------------------ reset
@@ -1132,38 +1130,6 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     legal_body(S, env, l, seat, off, cell, bits, rotl, nullptr, nullptr, counts, mask_words, mask_bool);
 }
 
-// One env-step's state work by one wave per env: the ply (k_step), the restart
-// of a finished game from the setup pool (k_reset_terminated, if do_reset) and
-// the legal sets of the next acting seat (k_legal with the current
-// turn), on the board the wave keeps in LDS, with no global round trip between
-// the three.
-__global__ __launch_bounds__(64) void k_env_step(State S, const int32_t *__restrict__ actions, StepOut O,
-                                                 int do_reset, int64_t reset_seed, int32_t *__restrict__ counts,
-                                                 int32_t *__restrict__ mask_words)
-{
-    const int env = blockIdx.x, l = threadIdx.x;
-    if (env >= S.n) return;
-    __shared__ int8_t cell[CELL_STRIDE];
-    __shared__ int16_t pos[PID_STRIDE];
-    __shared__ int8_t ptype[PID_STRIDE];
-    __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
-    __shared__ uint8_t rotl[NONB + 3];
-    TurnAfter nx;
-    step_env(S, env, l, actions, nullptr, 0, O, cell, pos, ptype, nx);
-    __syncthreads();
-    if (do_reset && S.pool_size > 0 && nx.term) {
-        init_env(S, env, S.pool + (size_t)reset_pool_index(env, reset_seed, S.pool_size) * NP, cell, pos, ptype);
-        nx.turn = 0; nx.term = false; nx.sdead = 0;
-    }
-    const int seat = nx.turn;
-    const bool off = nx.term || seat < 0 || seat > 3 || ((nx.sdead >> (seat & 3)) & 1);
-    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
-    if (mask_words)
-        for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[seat & 3][c];
-    __syncthreads();
-    legal_body(S, env, l, seat, off, cell, bits, rotl, pos, ptype, counts, mask_words, nullptr);
-}
-
 // Exclusive scan of counts into offsets (N+1); one 1024-thread block walks the
 // array in tiles of 32768 (one tile at the usual batch sizes): each thread
 // loads 32 consecutive counts with 16-byte loads, scans them in registers, the
@@ -1385,17 +1351,66 @@ __device__ __forceinline__ uint32_t philox4x32_10(uint32_t c0, uint32_t c1, uint
     return c0;
 }
 
+// Uniform pick from env's CSR row: Philox4x32-10 word 0 of counter
+// (env, ply lo, ply hi, 0) under key (seed lo, seed hi), scaled to the count;
+// -1 for an empty row.
+__device__ __forceinline__ int32_t sample_pick(int env, const int32_t *__restrict__ counts,
+                                               const int32_t *__restrict__ offsets, const int32_t *__restrict__ values,
+                                               uint64_t seed, uint64_t ply)
+{
+    const int c = counts[env];
+    if (c <= 0) return -1;
+    const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
+                                     (uint32_t)seed, (uint32_t)(seed >> 32));
+    const int idx = (int)(((uint64_t)u * (uint64_t)c) >> 32);
+    return values[offsets[env] + idx];
+}
+
 __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
                          const int32_t *__restrict__ values, uint64_t seed, uint64_t ply, int32_t *__restrict__ out)
 {
     const int env = blockIdx.x * blockDim.x + threadIdx.x;
     if (env >= n) return;
-    const int c = counts[env];
-    if (c <= 0) { out[env] = -1; return; }
-    const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
-                                     (uint32_t)seed, (uint32_t)(seed >> 32));
-    const int idx = (int)(((uint64_t)u * (uint64_t)c) >> 32);
-    out[env] = values[offsets[env] + idx];
+    out[env] = sample_pick(env, counts, offsets, values, seed, ply);
 }
+
+// One env-step's state work by one wave per env: the action (given, or the
+// Philox pick of k_sample from the env's previous CSR row, read before this
+// wave overwrites the env's count), the ply (k_step), the restart
+// of a finished game from the setup pool (k_reset_terminated, if do_reset) and
+// the legal sets of the next acting seat (k_legal with the current
+// turn), on the board the wave keeps in LDS, with no global round trip between
+// the three.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_env_step(State S, const int32_t *__restrict__ actions, uint64_t sample_seed,
+                                                 uint64_t ply, const int32_t *__restrict__ offsets,
+                                                 const int32_t *__restrict__ values, int32_t *__restrict__ actions_out,
+                                                 StepOut O, int do_reset, int64_t reset_seed,
+                                                 int32_t *__restrict__ counts, int32_t *__restrict__ mask_words)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    const int32_t a = actions ? actions[env] : sample_pick(env, counts, offsets, values, sample_seed, ply);
+    if (actions_out && l == 0) actions_out[env] = a;
+    __shared__ int8_t cell[CELL_STRIDE];
+    __shared__ int16_t pos[PID_STRIDE];
+    __shared__ int8_t ptype[PID_STRIDE];
+    __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
+    __shared__ uint8_t rotl[NONB + 3];
+    TurnAfter nx;
+    step_env(S, env, l, a, nullptr, 0, O, cell, pos, ptype, nx);
+    __syncthreads();
+    if (do_reset && S.pool_size > 0 && nx.term) {
+        init_env(S, env, S.pool + (size_t)reset_pool_index(env, reset_seed, S.pool_size) * NP, cell, pos, ptype);
+        nx.turn = 0; nx.term = false; nx.sdead = 0;
+    }
+    const int seat = nx.turn;
+    const bool off = nx.term || seat < 0 || seat > 3 || ((nx.sdead >> (seat & 3)) & 1);
+    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
+    if (mask_words)
+        for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[seat & 3][c];
+    __syncthreads();
+    legal_body(S, env, l, seat, off, cell, bits, rotl, pos, ptype, counts, mask_words, nullptr);
+}
+
 
 }  // namespace jq

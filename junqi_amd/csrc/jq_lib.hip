@@ -27,7 +27,6 @@ struct jq_env {
     State S{};
     std::vector<void *> allocs;
     bool zob_ready = false, rlut_ready = false;
-    int32_t *tmp_actions = nullptr;
     int obs_blocks = 0;              // resident u8 observation blocks on the device
     float *ext_bel = nullptr;        // uploaded (N, 4, 12, 289) beliefs, allocated on first upload
     bool ext_on = false;             // observations read the uploaded beliefs
@@ -253,7 +252,6 @@ int jq_create(jq_env **out, int32_t n, int32_t max_num_moves, int32_t show_mode,
     A(S.env, N, 0);
     A(S.hist, N * HIST_LEN, 0);
     A(S.lg, N, 0);
-    A(e->tmp_actions, N, 0);
     uint64_t *zt = nullptr; A(zt, (size_t)ZTOTAL, 0); S.ztab = zt;
     float *rl = nullptr; A(rl, 4 * 4096, 0); S.rlut = rl;
     hipLaunchKernelGGL(k_clear, dim3(n), dim3(64), 0, 0, S);
@@ -523,19 +521,14 @@ int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_
     int rc = check_env(e);
     if (rc) return rc;
     if (!counts || !offsets || !values) return fail(JQ_E_ARG, "env_step needs counts, offsets and values");
-    const int32_t *act = actions;
-    if (!act) {
-        int32_t *dst = actions_out ? actions_out : e->tmp_actions;
-        if ((rc = jq_sample_uniform(e, counts, offsets, values, sample_seed, ply, dst, stream)) != 0) return rc;
-        act = dst;
-    }
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before stepping");
     StepOut O = {};
     O.term = terminated;
     O.reward = reward;
-    // ply, restart from the pool and the next seat's legal sets in one kernel
-    hipLaunchKernelGGL(k_env_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, act, O, e->S.pool ? 1 : 0,
-                       reset_seed, counts, mask_words);
+    // sample (unless actions are given), ply, restart from the pool and the
+    // next seat's legal sets in one kernel
+    hipLaunchKernelGGL(k_env_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, actions, sample_seed, ply,
+                       offsets, values, actions_out, O, e->S.pool ? 1 : 0, reset_seed, counts, mask_words);
     if ((rc = launch_check("k_env_step")) != 0) return rc;
     hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, strm(stream), counts, offsets, e->S.n);
     if ((rc = launch_check("k_scan")) != 0) return rc;
