@@ -549,8 +549,10 @@ __device__ __forceinline__ uint4 obs_chunk(const ObsLds &L, int e0, int off, boo
                 w[i] = L.decb[c0] | (L.decb[c1] << 16);
             }
         } else {
-            for (int i = 0; i < 4; ++i)
-                w[i] = (((v >> (2 * i)) & 1u) ? 0x3F80u : 0u) | (((v >> (2 * i + 1)) & 1u) ? 0x3F800000u : 0u);
+            for (int i = 0; i < 4; ++i) {   // 2 bits -> two bf16 halves of 0 / 1.0
+                const uint32_t t = (v >> (2 * i)) & 3u;
+                w[i] = __umul24((t | (t << 15)) & 0x10001u, 0x3F80u);
+            }
         }
     } else {
         if (img) {
@@ -577,7 +579,9 @@ __device__ __forceinline__ void obs_elems(const ObsLds &L, uint8_t *row, int e, 
 }
 
 // Stream the 91,613-element row to `row` (element phase m) in 16-byte chunks:
-// chunk q covers row bytes [16q - lead, 16q - lead + 16).
+// chunk q covers row bytes [16q - lead, 16q - lead + 16). A wave iteration
+// stores one whole 1 KB-aligned unit of the buffer (the row's first and last
+// units in part); each wave owns a contiguous run of units.
 template <int FMT, bool EXT = false>
 __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m, const ExtLds *X = nullptr)
 {
@@ -590,15 +594,35 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m, const ExtLds *X =
     const int d2 = RG2_B + 16 + ((RG2_S + m) & 15) - RG2_S, d3 = RG3_B + 16 + ((RG3_S + m) & 15) - RG3_S;
     const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    for (int qb = qf + wv * 64; qb < ql; qb += OBS_THREADS) {
-        // the wave's span: chunk starts s_lo .. s_hi - EPC (uniform)
-        const int s_lo = qb * EPC - m, s_hi = min(qb + 64, ql) * EPC - m;
+    constexpr int NW = OBS_THREADS / 64;
+    const uint64_t gbase = (uint64_t)(uintptr_t)(row - lead) >> 4;
+    const uint64_t gA = gbase + qf, gB = gbase + ql;
+    const uint64_t u0 = gA >> 6, u1 = (gB + 63) >> 6;
+    const int nu = (int)(u1 - u0);
+    const int per = (nu + NW - 1) / NW;
+    const int ka = min(nu, wv * per), kb = min(nu, ka + per);
+    for (int k = ka; k < kb; ++k) {
+        const int qb = (int)((int64_t)((u0 + k) << 6) - (int64_t)gbase);
+        const int s_lo = max(qb, qf) * EPC - m, s_hi = min(qb + 64, ql) * EPC - m;
         const int q = qb + lane;
+        const bool ok = q >= qf && q < ql;
         const int e0 = q * EPC - m;
         uint8_t *dst = row + (ptrdiff_t)e0 * ES;
         if (FMT != 2 && ((s_lo < CT0_E && s_hi > CT0_S) || (s_lo < CT1_E && s_hi > CT1_S) ||
                          (EXT && ((s_lo < EB0_E && s_hi > EB0_S) || (s_lo < EB1_E && s_hi > EB1_S))))) {
-            if (q < ql) obs_elems<FMT, EXT>(L, row, e0, e0 + EPC, m, X);
+            if (ok) {   // per-element values, one 16-byte store
+                uint32_t w[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (FMT == 0) {
+                        w[i] = obs_elem<FMT, EXT>(L, e0 + i, m, X);
+                    } else {
+                        w[i] = obs_elem<FMT, EXT>(L, e0 + 2 * i, m, X) |
+                               (obs_elem<FMT, EXT>(L, e0 + 2 * i + 1, m, X) << 16);
+                    }
+                }
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+            }
             continue;
         }
         int nov = 0, d = 0, rs = 0, re = 0;
@@ -606,7 +630,7 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m, const ExtLds *X =
         if (s_lo < RG1_E && s_hi > RG1_S) { ++nov; d = d1; rs = RG1_S; re = RG1_E; }
         if (s_lo < RG2_E && s_hi > RG2_S) { ++nov; d = d2; rs = RG2_S; re = RG2_E; }
         if (s_lo < RG3_E && s_hi > RG3_S) { ++nov; d = d3; rs = RG3_S; re = RG3_E; }
-        if (q >= ql) continue;
+        if (!ok) continue;
         uint4 out;
         if (nov == 0) {
             out = obs_chunk<FMT>(L, e0, IMG_ZERO, false);
