@@ -36,18 +36,29 @@ struct alignas(16) PieceRec {
 };
 static_assert(sizeof(PieceRec) == 16, "piece record must be 16 bytes");
 
-// CombatMemory v6 of one (observer, pid) (combat_memory.py:251-311).
+// CombatMemory v6 of one (observer, pid) (combat_memory.py:251-311), in three
+// arrays indexed alike (cm_idx): the record the observation reads for enemy
+// pieces, the eaten-by set it reads for the observer's own pieces, and a byte
+// summary (kill count capped at 3, flags) it reads where only that is used.
 struct alignas(16) CmRec {
     uint64_t dlo, dhi;       // pids killed directly (120-bit set)
     uint64_t clo, chi;       // pids killed directly or by chain
-    uint64_t elo, ehi;       // pids this (own) piece was eaten by
     uint16_t dtype, ctype;   // tracked types killed directly / by chain (12 bits)
     int16_t ldir, ocnt, lchain, fstep;  // last direct step, other count, last chain step, floor step
     int8_t floor;
     uint8_t flags;           // CMF_*
     uint16_t pad;
 };
-static_assert(sizeof(CmRec) == 64, "combat-memory record must be 64 bytes");
+static_assert(sizeof(CmRec) == 48, "combat-memory record must be 48 bytes");
+struct alignas(16) CmEat {
+    uint64_t elo, ehi;       // pids this (own) piece was eaten by
+};
+// summary byte: min(|killed directly| + other count, 3) | flags << 2
+__device__ __forceinline__ uint8_t cm_summary(const CmRec &c)
+{
+    const int n = __popcll(c.dlo) + __popcll(c.dhi) + c.ocnt;
+    return (uint8_t)((n < 3 ? n : 3) | ((c.flags & 7) << 2));
+}
 
 // Per-env scalars.
 struct alignas(16) EnvRec {
@@ -79,6 +90,8 @@ struct State {
     int8_t *cell;          // [n][292]
     PieceRec *piece;       // [n][128]
     CmRec *cm;             // [n][4][128]
+    CmEat *cme;            // [n][4][128]
+    uint8_t *cmk;          // [n][4][128] cm_summary of cm
     uint8_t *bcode;        // [n][4][128]
     int8_t *rem;           // [n][4][4][12]
     EnvRec *env;           // [n]

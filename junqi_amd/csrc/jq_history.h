@@ -10,9 +10,11 @@
 namespace jq {
 
 // Per-env bytes of one history row: board, piece records, all four observers'
-// combat memory and belief codes, remaining counts, env record, move ring.
-constexpr size_t HIST_ROW_BYTES = CELL_STRIDE + PID_STRIDE * sizeof(PieceRec) + 4 * PID_STRIDE * sizeof(CmRec) +
-                                  4 * PID_STRIDE + 4 * 48 + sizeof(EnvRec) + HIST_LEN * sizeof(int32_t);
+// combat memory (records and eaten-by sets; the summary bytes are derived on
+// gather) and belief codes, remaining counts, env record, move ring.
+constexpr size_t HIST_ROW_BYTES = CELL_STRIDE + PID_STRIDE * sizeof(PieceRec) +
+                                  4 * PID_STRIDE * (sizeof(CmRec) + sizeof(CmEat)) + 4 * PID_STRIDE + 4 * 48 +
+                                  sizeof(EnvRec) + HIST_LEN * sizeof(int32_t);
 
 // History arrays, row r = step * n + env, each laid out like the State array
 // of the same name.
@@ -21,6 +23,7 @@ struct HistState {
     int8_t *cell;
     PieceRec *piece;
     CmRec *cm;
+    CmEat *cme;
     uint8_t *bcode;
     int8_t *rem;
     EnvRec *env;
@@ -50,7 +53,12 @@ __global__ __launch_bounds__(256) void k_history_gather(HistState H, const int64
     copy_words(reinterpret_cast<uint4 *>(R.piece + (size_t)i * PID_STRIDE),
                reinterpret_cast<const uint4 *>(H.piece + (size_t)f * PID_STRIDE), PID_STRIDE, t, 256);
     copy_words(reinterpret_cast<uint4 *>(R.cm + (size_t)i * 4 * PID_STRIDE),
-               reinterpret_cast<const uint4 *>(H.cm + (size_t)f * 4 * PID_STRIDE), 4 * PID_STRIDE * 4, t, 256);
+               reinterpret_cast<const uint4 *>(H.cm + (size_t)f * 4 * PID_STRIDE),
+               4 * PID_STRIDE * (int)(sizeof(CmRec) / 16), t, 256);
+    copy_words(reinterpret_cast<uint4 *>(R.cme + (size_t)i * 4 * PID_STRIDE),
+               reinterpret_cast<const uint4 *>(H.cme + (size_t)f * 4 * PID_STRIDE), 4 * PID_STRIDE, t, 256);
+    for (int k = t; k < 4 * PID_STRIDE; k += 256)   // the summaries are not stored: derive them
+        R.cmk[(size_t)i * 4 * PID_STRIDE + k] = cm_summary(H.cm[(size_t)f * 4 * PID_STRIDE + k]);
     copy_words(reinterpret_cast<uint4 *>(R.bcode + (size_t)i * 4 * PID_STRIDE),
                reinterpret_cast<const uint4 *>(H.bcode + (size_t)f * 4 * PID_STRIDE), 4 * PID_STRIDE / 16, t, 256);
     copy_words(reinterpret_cast<uint4 *>(R.rem + (size_t)i * 4 * 48),

@@ -558,8 +558,8 @@ __device__ __forceinline__ void cm_apply(const State &S, int env, bool is_eat, i
         uint64_t vlo = (v.dlo | v.clo) & mlo, vhi = (v.dhi | v.chi) & mhi;
         if (Vs == o) { if (V < 64) vlo |= 1ull << V; else vhi |= 1ull << (V - 64); }
         const uint64_t klo = K < 64 ? (1ull << K) : 0ull, khi = K >= 64 ? (1ull << (K - 64)) : 0ull;
-        while (vlo) { const int b = __builtin_ctzll(vlo); vlo &= vlo - 1; CmRec &t = S.cm[cm_idx(env, o, b)]; t.elo |= klo; t.ehi |= khi; }
-        while (vhi) { const int b = __builtin_ctzll(vhi) + 64; vhi &= vhi - 1; CmRec &t = S.cm[cm_idx(env, o, b)]; t.elo |= klo; t.ehi |= khi; }
+        while (vlo) { const int b = __builtin_ctzll(vlo); vlo &= vlo - 1; CmEat &t = S.cme[cm_idx(env, o, b)]; t.elo |= klo; t.ehi |= khi; }
+        while (vhi) { const int b = __builtin_ctzll(vhi) + 64; vhi &= vhi - 1; CmEat &t = S.cme[cm_idx(env, o, b)]; t.elo |= klo; t.ehi |= khi; }
     }
     if (Vs != o) {
         const int c = k.ocnt + 1;
@@ -580,6 +580,7 @@ __device__ __forceinline__ void cm_apply(const State &S, int env, bool is_eat, i
     k.ldir = (int16_t)step;
     k.lchain = (int16_t)step;
     S.cm[kI] = k;
+    S.cmk[kI] = cm_summary(k);
 }
 
 // BeliefTensor.update for the four observers (info_model.py:271-429). Entries are
@@ -696,7 +697,10 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     const int ss = sp / 30, ds = dp >= 0 ? dp / 30 : -1;
 
     if (st == T_GONGB && engineer_only(cell, src, dst)) {
-        if (l < 4) S.cm[cm_idx(env, l, sp)].flags |= CMF_IS_GONGB;
+        if (l < 4) {
+            S.cm[cm_idx(env, l, sp)].flags |= CMF_IS_GONGB;
+            S.cmk[cm_idx(env, l, sp)] |= (uint8_t)(CMF_IS_GONGB << 2);
+        }
     }
     // move history (state.py:673-678)
     const int hcnt = E.hmeta & 0xFF, hhead = (E.hmeta >> 8) & 31;
@@ -820,10 +824,13 @@ __device__ __forceinline__ void clear_env(const State &S, int env, int t, int nt
     r.ptype = r.dreason = -1;
     CmRec c = {};
     c.ldir = c.lchain = c.fstep = -1;
+    const CmEat ce = {};
     for (int p = t; p < PID_STRIDE; p += nt) {
         S.piece[pc_idx(env, p)] = r;
         for (int o = 0; o < 4; ++o) {
             S.cm[cm_idx(env, o, p)] = c;
+            S.cme[cm_idx(env, o, p)] = ce;
+            S.cmk[cm_idx(env, o, p)] = 0;
             S.bcode[((size_t)env * 4 + o) * PID_STRIDE + p] = 0;
         }
     }
@@ -886,6 +893,8 @@ __device__ void init_env(const State &S, int env, const int8_t *types, int8_t *l
             CmRec c = {};
             c.ldir = -1; c.lchain = -1; c.fstep = -1;
             S.cm[cm_idx(env, o, p)] = c;
+            S.cme[cm_idx(env, o, p)] = CmEat{};
+            S.cmk[cm_idx(env, o, p)] = 0;
         }
     }
     z = wave_xor(z);
@@ -946,6 +955,7 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
         const PieceRec r = S.piece[pi];
         const int f = r.pos, t = r.ptype;
         if (f >= 0 && t >= 0) z ^= zp(S.ztab, p, t, f);
+        for (int o = 0; o < 4; ++o) S.cmk[cm_idx(env, o, p)] = cm_summary(S.cm[cm_idx(env, o, p)]);
         for (int o = 0; o < 4 && beliefs; ++o) {
             uint8_t code = 0;
             if (f >= 0 && t >= 2) {

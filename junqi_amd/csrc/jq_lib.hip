@@ -156,10 +156,11 @@ int halloc(jq_history *h, T *&p, size_t count)
 
 // Where field f lives: array, per-env stride, element stride, byte offset of
 // element 0 inside its record, element size, elements per env.
-enum FieldArr { AR_CELL, AR_PIECE, AR_CM, AR_BCODE, AR_REM, AR_ENV, AR_HIST };
+enum FieldArr { AR_CELL, AR_PIECE, AR_CM, AR_CME, AR_BCODE, AR_REM, AR_ENV, AR_HIST };
 struct FieldDesc { int arr, elems, bytes; size_t env_stride, el_stride, off; };
 #define PF(m) {AR_PIECE, PID_STRIDE, (int)sizeof(PieceRec::m), PID_STRIDE * sizeof(PieceRec), sizeof(PieceRec), offsetof(PieceRec, m)}
 #define CF(m) {AR_CM, 4 * PID_STRIDE, (int)sizeof(CmRec::m), 4 * PID_STRIDE * sizeof(CmRec), sizeof(CmRec), offsetof(CmRec, m)}
+#define CE(m) {AR_CME, 4 * PID_STRIDE, (int)sizeof(CmEat::m), 4 * PID_STRIDE * sizeof(CmEat), sizeof(CmEat), offsetof(CmEat, m)}
 #define EF(m) {AR_ENV, 1, (int)sizeof(EnvRec::m), sizeof(EnvRec), sizeof(EnvRec::m), offsetof(EnvRec, m)}
 const FieldDesc kFields[JQ_F_COUNT] = {
     {AR_CELL, CELL_STRIDE, 1, CELL_STRIDE, 1, 0},
@@ -167,13 +168,14 @@ const FieldDesc kFields[JQ_F_COUNT] = {
     {AR_BCODE, 4 * PID_STRIDE, 1, 4 * PID_STRIDE, 1, 0},
     {AR_REM, 4 * 48, 1, 4 * 48, 1, 0},
     {AR_ENV, 4, 1, sizeof(EnvRec), 1, offsetof(EnvRec, remtrk)},
-    CF(dlo), CF(dhi), CF(dtype), CF(ldir), CF(ocnt), CF(clo), CF(chi), CF(ctype), CF(lchain), CF(elo), CF(ehi),
+    CF(dlo), CF(dhi), CF(dtype), CF(ldir), CF(ocnt), CF(clo), CF(chi), CF(ctype), CF(lchain), CE(elo), CE(ehi),
     CF(floor), CF(fstep), CF(flags),
     {AR_HIST, HIST_LEN, 4, HIST_LEN * 4, 4, 0},
     EF(hmeta), EF(turn), EF(term), EF(winner), EF(draw), EF(sdead), EF(sflag), EF(mc), EF(mslc), EF(zob),
 };
 #undef PF
 #undef CF
+#undef CE
 #undef EF
 
 uint8_t *field_array(jq_env *e, int arr)
@@ -183,6 +185,7 @@ uint8_t *field_array(jq_env *e, int arr)
     case AR_CELL: return reinterpret_cast<uint8_t *>(S.cell);
     case AR_PIECE: return reinterpret_cast<uint8_t *>(S.piece);
     case AR_CM: return reinterpret_cast<uint8_t *>(S.cm);
+    case AR_CME: return reinterpret_cast<uint8_t *>(S.cme);
     case AR_BCODE: return S.bcode;
     case AR_REM: return reinterpret_cast<uint8_t *>(S.rem);
     case AR_ENV: return reinterpret_cast<uint8_t *>(S.env);
@@ -247,6 +250,8 @@ int jq_create(jq_env **out, int32_t n, int32_t max_num_moves, int32_t show_mode,
     A(S.cell, N * CELL_STRIDE, 0xFF);
     A(S.piece, N * PID_STRIDE, 0);
     A(S.cm, N * 4 * PID_STRIDE, 0);
+    A(S.cme, N * 4 * PID_STRIDE, 0);
+    A(S.cmk, N * 4 * PID_STRIDE, 0);
     A(S.bcode, N * 4 * PID_STRIDE, 0);
     A(S.rem, N * 4 * 48, 0);
     A(S.env, N, 0);
@@ -640,6 +645,7 @@ int jq_history_create(jq_history **out, int32_t num_envs, int32_t num_steps, int
     A(H.cell, R * CELL_STRIDE);
     A(H.piece, R * PID_STRIDE);
     A(H.cm, R * 4 * PID_STRIDE);
+    A(H.cme, R * 4 * PID_STRIDE);
     A(H.bcode, R * 4 * PID_STRIDE);
     A(H.rem, R * 4 * 48);
     A(H.env, R);
@@ -684,6 +690,7 @@ int jq_history_snapshot(jq_history *h, jq_env *e, const int8_t *acting, int32_t 
     HIP_TRY(hipMemcpyAsync(H.cell + r0 * CELL_STRIDE, S.cell, n * CELL_STRIDE, hipMemcpyDeviceToDevice, s));
     HIP_TRY(hipMemcpyAsync(H.piece + r0 * PID_STRIDE, S.piece, n * PID_STRIDE * sizeof(PieceRec), hipMemcpyDeviceToDevice, s));
     HIP_TRY(hipMemcpyAsync(H.cm + r0 * 4 * PID_STRIDE, S.cm, n * 4 * PID_STRIDE * sizeof(CmRec), hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(H.cme + r0 * 4 * PID_STRIDE, S.cme, n * 4 * PID_STRIDE * sizeof(CmEat), hipMemcpyDeviceToDevice, s));
     HIP_TRY(hipMemcpyAsync(H.bcode + r0 * 4 * PID_STRIDE, S.bcode, n * 4 * PID_STRIDE, hipMemcpyDeviceToDevice, s));
     HIP_TRY(hipMemcpyAsync(H.rem + r0 * 4 * 48, S.rem, n * 4 * 48, hipMemcpyDeviceToDevice, s));
     HIP_TRY(hipMemcpyAsync(H.env + r0, S.env, n * sizeof(EnvRec), hipMemcpyDeviceToDevice, s));

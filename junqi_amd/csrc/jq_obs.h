@@ -151,8 +151,7 @@ struct PieceIn {
     uint64_t dlo, dhi, clo, chi;   // observer's combat memory (enemy pieces)
     int dtype, ctype, ocnt, floor, flags, ldir, lchain, fstep;
     uint64_t elo, ehi;             // eaten_by of the observer's own pieces
-    uint64_t ldlo, ldhi, rdlo, rdhi;  // left / right enemies' memory of an own piece
-    int locnt, rocnt, lflags, rflags;
+    int lsum, rsum;                // left / right enemies' memory of an own piece (cm_summary)
 };
 
 __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int pid, PieceIn &P)
@@ -163,10 +162,10 @@ __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int
     P.mcount = r.mcount; P.aeat = r.aeat; P.psurv = r.psurv;
     P.dstep = r.dstep; P.dreason = r.dreason; P.dloc = r.dloc; P.zero = r.zero;
     P.bcode = S.bcode[((size_t)env * 4 + obs) * PID_STRIDE + pid];
-    P.dlo = P.dhi = P.clo = P.chi = P.elo = P.ehi = P.ldlo = P.ldhi = P.rdlo = P.rdhi = 0;
+    P.dlo = P.dhi = P.clo = P.chi = P.elo = P.ehi = 0;
     P.dtype = P.ctype = P.ocnt = P.floor = P.flags = 0;
     P.ldir = P.lchain = P.fstep = -1;
-    P.locnt = P.rocnt = P.lflags = P.rflags = 0;
+    P.lsum = P.rsum = 0;
     if ((s & 1) != (obs & 1)) {
         const CmRec c = S.cm[cm_idx(env, obs, pid)];
         P.dlo = c.dlo; P.dhi = c.dhi; P.clo = c.clo; P.chi = c.chi;
@@ -174,11 +173,10 @@ __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int
         P.floor = c.floor; P.flags = c.flags;
         P.ldir = c.ldir; P.lchain = c.lchain; P.fstep = c.fstep;
     } else if (s == obs) {
-        const CmRec &c = S.cm[cm_idx(env, obs, pid)];
-        P.elo = c.elo; P.ehi = c.ehi;
-        const CmRec &lc = S.cm[cm_idx(env, le, pid)], &rc = S.cm[cm_idx(env, re, pid)];
-        P.ldlo = lc.dlo; P.ldhi = lc.dhi; P.locnt = lc.ocnt; P.lflags = lc.flags;
-        P.rdlo = rc.dlo; P.rdhi = rc.dhi; P.rocnt = rc.ocnt; P.rflags = rc.flags;
+        const CmEat e = S.cme[cm_idx(env, obs, pid)];
+        P.elo = e.elo; P.ehi = e.ehi;
+        P.lsum = S.cmk[cm_idx(env, le, pid)];
+        P.rsum = S.cmk[cm_idx(env, re, pid)];
     }
 }
 
@@ -260,13 +258,13 @@ __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, i
                 if (c) set_code(L, RG3_B, RG3_S, (211 + q) * NC + k, m,
                                 c == 1 ? CODE_THIRD : c == 2 ? CODE_2THIRD : CODE_ONE);
             }
-        } else if (s == obs) {   // layer 2 (observation.py:1392-1451)
-            const int lc = __popcll(P.ldlo) + __popcll(P.ldhi) + P.locnt;
-            const int rcnt = __popcll(P.rdlo) + __popcll(P.rdhi) + P.rocnt;
+        } else if (s == obs) {   // layer 2 (observation.py:1392-1451); counts capped at 3
+            const int lc = P.lsum & 3, rcnt = P.rsum & 3;
+            const int lflags = P.lsum >> 2, rflags = P.rsum >> 2;
             const int pk = lc < rcnt ? lc : rcnt;
             for (int q = 0; q < 3; ++q) if (pk >= q + 1) cmb |= 1ull << (45 + q);
-            if ((P.lflags & CMF_IS_GONGB) && (P.rflags & CMF_IS_GONGB)) cmb |= 1ull << 48;
-            const bool atk = (P.lflags & CMF_ATK_GONGB) || (P.rflags & CMF_ATK_GONGB);
+            if ((lflags & CMF_IS_GONGB) && (rflags & CMF_IS_GONGB)) cmb |= 1ull << 48;
+            const bool atk = (lflags & CMF_ATK_GONGB) || (rflags & CMF_ATK_GONGB);
             if (back_two(s, P.zero) && P.mcount == 0 && !atk) cmb |= 1ull << 49;
         }
         while (cmb) {   // combat-memory bit planes 161-210
