@@ -56,8 +56,36 @@ struct alignas(16) CmEat {
 // summary byte: min(|killed directly| + other count, 3) | flags << 2
 __device__ __forceinline__ uint8_t cm_summary(const CmRec &c)
 {
-    const int n = __popcll(c.dlo) + __popcll(c.dhi) + c.ocnt;
+    const int n = __popcll(c.dlo) + __popcll(c.dhi) + (c.ocnt > 0 ? c.ocnt : 0);
     return (uint8_t)((n < 3 ? n : 3) | ((c.flags & 7) << 2));
+}
+
+// What the observation of observer o uses of record (o, pid) for an enemy
+// piece, derived from the record: the observer's own pieces it killed
+// directly, types killed, floor, flags, counts capped at 3, recency steps.
+struct alignas(16) CmView {
+    uint32_t kmask;          // bit s: pid o*30 + s killed directly
+    uint32_t types;          // dtype | ctype << 12 | floor << 24 | flags << 28
+    uint16_t cnts;           // min(|direct|, 3) | min(|chain|, 3) << 2 | min(other, 3) << 4
+    int16_t ldir, lchain, fstep;
+};
+static_assert(sizeof(CmView) == 16, "combat-memory view must be 16 bytes");
+
+__device__ __forceinline__ CmView cm_view(const CmRec &c, int o)
+{
+    const int b = o * 30;   // the 30 pids of seat o in the 128-bit pid set (dlo, dhi)
+    const uint64_t w = b == 0 ? c.dlo : b < 64 ? ((c.dlo >> b) | (c.dhi << (64 - b))) : (c.dhi >> (b - 64));
+    const uint32_t k = (uint32_t)w & 0x3FFFFFFFu;
+    const int m = __popcll(c.dlo) + __popcll(c.dhi), ch = __popcll(c.clo) + __popcll(c.chi);
+    CmView v;
+    v.kmask = k;
+    const int fl = c.floor < 0 ? 0 : c.floor < 9 ? c.floor : 9;
+    v.types = (uint32_t)(c.dtype & 0xFFF) | ((uint32_t)(c.ctype & 0xFFF) << 12) | ((uint32_t)fl << 24) |
+              ((uint32_t)(c.flags & 7) << 28);
+    const int oc = c.ocnt < 0 ? 0 : c.ocnt < 3 ? c.ocnt : 3;
+    v.cnts = (uint16_t)((m < 3 ? m : 3) | ((ch < 3 ? ch : 3) << 2) | (oc << 4));
+    v.ldir = c.ldir; v.lchain = c.lchain; v.fstep = c.fstep;
+    return v;
 }
 
 // Per-env scalars.
@@ -92,6 +120,7 @@ struct State {
     CmRec *cm;             // [n][4][128]
     CmEat *cme;            // [n][4][128]
     uint8_t *cmk;          // [n][4][128] cm_summary of cm
+    CmView *cmv;           // [n][4][128] cm_view of cm for its observer
     uint8_t *bcode;        // [n][4][128]
     int8_t *rem;           // [n][4][4][12]
     EnvRec *env;           // [n]

@@ -57,8 +57,11 @@ __global__ __launch_bounds__(256) void k_history_gather(HistState H, const int64
                4 * PID_STRIDE * (int)(sizeof(CmRec) / 16), t, 256);
     copy_words(reinterpret_cast<uint4 *>(R.cme + (size_t)i * 4 * PID_STRIDE),
                reinterpret_cast<const uint4 *>(H.cme + (size_t)f * 4 * PID_STRIDE), 4 * PID_STRIDE, t, 256);
-    for (int k = t; k < 4 * PID_STRIDE; k += 256)   // the summaries are not stored: derive them
-        R.cmk[(size_t)i * 4 * PID_STRIDE + k] = cm_summary(H.cm[(size_t)f * 4 * PID_STRIDE + k]);
+    for (int k = t; k < 4 * PID_STRIDE; k += 256) {   // summaries and views are not stored: derive them
+        const CmRec c = H.cm[(size_t)f * 4 * PID_STRIDE + k];
+        R.cmk[(size_t)i * 4 * PID_STRIDE + k] = cm_summary(c);
+        R.cmv[(size_t)i * 4 * PID_STRIDE + k] = cm_view(c, k / PID_STRIDE);
+    }
     copy_words(reinterpret_cast<uint4 *>(R.bcode + (size_t)i * 4 * PID_STRIDE),
                reinterpret_cast<const uint4 *>(H.bcode + (size_t)f * 4 * PID_STRIDE), 4 * PID_STRIDE / 16, t, 256);
     copy_words(reinterpret_cast<uint4 *>(R.rem + (size_t)i * 4 * 48),

@@ -581,6 +581,7 @@ __device__ __forceinline__ void cm_apply(const State &S, int env, bool is_eat, i
     k.lchain = (int16_t)step;
     S.cm[kI] = k;
     S.cmk[kI] = cm_summary(k);
+    S.cmv[kI] = cm_view(k, o);
 }
 
 // BeliefTensor.update for the four observers (info_model.py:271-429). Entries are
@@ -700,6 +701,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
         if (l < 4) {
             S.cm[cm_idx(env, l, sp)].flags |= CMF_IS_GONGB;
             S.cmk[cm_idx(env, l, sp)] |= (uint8_t)(CMF_IS_GONGB << 2);
+            S.cmv[cm_idx(env, l, sp)].types |= (uint32_t)CMF_IS_GONGB << 28;
         }
     }
     // move history (state.py:673-678)
@@ -825,12 +827,14 @@ __device__ __forceinline__ void clear_env(const State &S, int env, int t, int nt
     CmRec c = {};
     c.ldir = c.lchain = c.fstep = -1;
     const CmEat ce = {};
+    const CmView cv = cm_view(c, 0);
     for (int p = t; p < PID_STRIDE; p += nt) {
         S.piece[pc_idx(env, p)] = r;
         for (int o = 0; o < 4; ++o) {
             S.cm[cm_idx(env, o, p)] = c;
             S.cme[cm_idx(env, o, p)] = ce;
             S.cmk[cm_idx(env, o, p)] = 0;
+            S.cmv[cm_idx(env, o, p)] = cv;
             S.bcode[((size_t)env * 4 + o) * PID_STRIDE + p] = 0;
         }
     }
@@ -895,6 +899,7 @@ __device__ void init_env(const State &S, int env, const int8_t *types, int8_t *l
             S.cm[cm_idx(env, o, p)] = c;
             S.cme[cm_idx(env, o, p)] = CmEat{};
             S.cmk[cm_idx(env, o, p)] = 0;
+            S.cmv[cm_idx(env, o, p)] = cm_view(c, o);
         }
     }
     z = wave_xor(z);
@@ -955,7 +960,11 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
         const PieceRec r = S.piece[pi];
         const int f = r.pos, t = r.ptype;
         if (f >= 0 && t >= 0) z ^= zp(S.ztab, p, t, f);
-        for (int o = 0; o < 4; ++o) S.cmk[cm_idx(env, o, p)] = cm_summary(S.cm[cm_idx(env, o, p)]);
+        for (int o = 0; o < 4; ++o) {
+            const CmRec c = S.cm[cm_idx(env, o, p)];
+            S.cmk[cm_idx(env, o, p)] = cm_summary(c);
+            S.cmv[cm_idx(env, o, p)] = cm_view(c, o);
+        }
         for (int o = 0; o < 4 && beliefs; ++o) {
             uint8_t code = 0;
             if (f >= 0 && t >= 2) {

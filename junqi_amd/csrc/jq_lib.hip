@@ -252,6 +252,7 @@ int jq_create(jq_env **out, int32_t n, int32_t max_num_moves, int32_t show_mode,
     A(S.cm, N * 4 * PID_STRIDE, 0);
     A(S.cme, N * 4 * PID_STRIDE, 0);
     A(S.cmk, N * 4 * PID_STRIDE, 0);
+    A(S.cmv, N * 4 * PID_STRIDE, 0);
     A(S.bcode, N * 4 * PID_STRIDE, 0);
     A(S.rem, N * 4 * 48, 0);
     A(S.env, N, 0);

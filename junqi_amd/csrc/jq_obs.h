@@ -148,8 +148,8 @@ __device__ __forceinline__ int canon_cell(int s, int f)
 // before the block's first barrier (observation.py:908-1620 per-piece writers).
 struct PieceIn {
     int pos, tp, mcount, aeat, psurv, dstep, dreason, dloc, zero, bcode;
-    uint64_t dlo, dhi, clo, chi;   // observer's combat memory (enemy pieces)
-    int dtype, ctype, ocnt, floor, flags, ldir, lchain, fstep;
+    uint32_t kmask, types, cnts;   // observer's combat memory of an enemy piece (CmView)
+    int ldir, lchain, fstep;
     uint64_t elo, ehi;             // eaten_by of the observer's own pieces
     int lsum, rsum;                // left / right enemies' memory of an own piece (cm_summary)
 };
@@ -162,16 +162,14 @@ __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int
     P.mcount = r.mcount; P.aeat = r.aeat; P.psurv = r.psurv;
     P.dstep = r.dstep; P.dreason = r.dreason; P.dloc = r.dloc; P.zero = r.zero;
     P.bcode = S.bcode[((size_t)env * 4 + obs) * PID_STRIDE + pid];
-    P.dlo = P.dhi = P.clo = P.chi = P.elo = P.ehi = 0;
-    P.dtype = P.ctype = P.ocnt = P.floor = P.flags = 0;
+    P.elo = P.ehi = 0;
+    P.kmask = P.types = P.cnts = 0;
     P.ldir = P.lchain = P.fstep = -1;
     P.lsum = P.rsum = 0;
     if ((s & 1) != (obs & 1)) {
-        const CmRec c = S.cm[cm_idx(env, obs, pid)];
-        P.dlo = c.dlo; P.dhi = c.dhi; P.clo = c.clo; P.chi = c.chi;
-        P.dtype = c.dtype; P.ctype = c.ctype; P.ocnt = c.ocnt;
-        P.floor = c.floor; P.flags = c.flags;
-        P.ldir = c.ldir; P.lchain = c.lchain; P.fstep = c.fstep;
+        const CmView v = S.cmv[cm_idx(env, obs, pid)];
+        P.kmask = v.kmask; P.types = v.types; P.cnts = v.cnts;
+        P.ldir = v.ldir; P.lchain = v.lchain; P.fstep = v.fstep;
     } else if (s == obs) {
         const CmEat e = S.cme[cm_idx(env, obs, pid)];
         P.elo = e.elo; P.ehi = e.ehi;
@@ -229,23 +227,23 @@ __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, i
 
         uint64_t cmb = 0;
         if (!ours) {   // combat-memory layers 1 and 3 (observation.py:1292-1387, 1475-1567)
-            const int mcnt = __popcll(P.dlo) + __popcll(P.dhi);
-            const int ccnt = __popcll(P.clo) + __popcll(P.chi);
-            cmb |= (uint64_t)(P.dtype & 0xFFF);
+            const int mcnt = P.cnts & 3, ccnt = (P.cnts >> 2) & 3, ocnt = (P.cnts >> 4) & 3;   // capped at 3
+            const int floor = (P.types >> 24) & 15, flags = P.types >> 28;
+            cmb |= (uint64_t)(P.types & 0xFFF);
             for (int q = 0; q < 3; ++q) {
                 if (mcnt >= q + 1) cmb |= 1ull << (12 + q);
-                if (P.ocnt >= q + 1) cmb |= 1ull << (15 + q);
+                if (ocnt >= q + 1) cmb |= 1ull << (15 + q);
                 if (ccnt >= q + 1) cmb |= 1ull << (30 + q);
             }
-            cmb |= (uint64_t)(P.ctype & 0xFFF) << 18;
-            for (int q = 0; q < 9; ++q) if (P.floor >= q + 1) cmb |= 1ull << (33 + q);
-            if (P.flags & CMF_IS_GONGB) cmb |= 1ull << 42;
-            if (P.flags & CMF_NOT_GONGB) cmb |= 1ull << 43;
-            if (back_two(s, P.zero) && P.mcount == 0 && !(P.flags & CMF_ATK_GONGB)) cmb |= 1ull << 44;
+            cmb |= (uint64_t)((P.types >> 12) & 0xFFF) << 18;
+            for (int q = 0; q < 9; ++q) if (floor >= q + 1) cmb |= 1ull << (33 + q);
+            if (flags & CMF_IS_GONGB) cmb |= 1ull << 42;
+            if (flags & CMF_NOT_GONGB) cmb |= 1ull << 43;
+            if (back_two(s, P.zero) && P.mcount == 0 && !(flags & CMF_ATK_GONGB)) cmb |= 1ull << 44;
             // kill_mine_slot (223-252) and kill_mine_count (211-222) over the
             // observer's own pieces this one has killed directly
             uint64_t tcnt = 0;   // 12 counters of 5 bits, one per tracked type
-            for (uint32_t hits = seat_bits(P.dlo, P.dhi, obs * 30); hits; hits &= hits - 1) {
+            for (uint32_t hits = P.kmask; hits; hits &= hits - 1) {
                 const int sl = __builtin_ctz(hits);
                 set_el(L, (223 + sl) * NC + k);
                 const uint32_t tw = sl < 8 ? own_types[0] : sl < 16 ? own_types[1] : sl < 24 ? own_types[2] : own_types[3];
