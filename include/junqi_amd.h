@@ -229,10 +229,14 @@ int jq_set_field(jq_env *env, int32_t field, const void *host_src);
 int jq_field_ptr(jq_env *env, int32_t field, void **dev_ptr, int64_t *env_stride, int64_t *elem_stride);
 /* After jq_set_field edits: recompute every env's Zobrist hash and re-seed the
  * four beliefs from the current board (GameState.__post_init__, state.py:346-483;
- * BeliefTensor.initial, info_model.py:218-265). */
+ * BeliefTensor.initial, info_model.py:218-265). Also rebuilds the compact
+ * combat-memory summaries the observation reads, so edits of JQ_F_CM_* fields
+ * (through jq_set_field or a jq_field_ptr view) reach observations only after
+ * this call or jq_rehash. */
 int jq_finalize_import(jq_env *env, void *stream);
-/* Recompute every env's Zobrist hash from its current fields (after editing
- * scalar fields such as the termination flags); beliefs are left as they are. */
+/* Recompute every env's Zobrist hash and combat-memory summaries from its
+ * current fields (after editing scalar fields such as the termination flags);
+ * beliefs are left as they are. */
 int jq_rehash(jq_env *env, void *stream);
 
 /* ---- compact rollout history ------------------------------------------------
