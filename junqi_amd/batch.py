@@ -299,6 +299,12 @@ class JunqiBatch:
     def finalize_import(self) -> None:
         check(lib.jq_finalize_import(self._h, self.stream))
 
+    def rehash(self) -> None:
+        """Zobrist hashes and combat-memory summaries from the current fields;
+        beliefs stay as set."""
+        check(lib.jq_rehash(self._h, self.stream))
+        torch.cuda.synchronize(self.device)
+
     def import_state(self, sd: dict, *, terminated=None, winner_team=None, draw=None,
                      move_history=None) -> None:
         """Load every env from the flat SoA dict that the reference's

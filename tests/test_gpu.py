@@ -356,6 +356,48 @@ def test_slot_mask_matches_oracle(jq):
     b.close()
 
 
+def test_imported_state_observes_like_the_oracle(jq):
+    """Every state field of oracle-played games (combat memory, beliefs and the
+    move ring included) set through jq_set_field, then jq_rehash: observations
+    of all four seats equal the oracle's bit for bit, so the compact
+    combat-memory summaries the observation reads are rebuilt from the import."""
+    games = []
+    for k in range(24):
+        g = O.Game(O.random_setup(300 + k), show_mode=2)
+        rng = np.random.default_rng(k)
+        for _ in range(30 + 8 * k):
+            ids = g.legal_ids()
+            if not len(ids) or g.terminated:
+                break
+            g.step_id(int(ids[rng.integers(len(ids))]))
+        games.append(g)
+    n = len(games)
+    print(f"[import] n={n}", flush=True)
+    b = jq.JunqiBatch(n, show_mode=2)
+    f = G.oracle_fields(games)
+    for name, v in f.items():
+        if name != "hist_list":
+            b.set_field(name, v)
+    ring = np.zeros((n, 32), np.int32)
+    meta = np.zeros((n, 1), np.int32)
+    for i, h in enumerate(f["hist_list"]):
+        for j, (src, dst) in enumerate(h):
+            ring[i, j] = src | (dst << 16)
+        meta[i, 0] = len(h) | ((len(h) & 31) << 8)
+    b.set_field("hist", ring)
+    b.set_field("hist_meta", meta)
+    b.rehash()
+    G.compare_state(G.device_fields(b), f, ctx="imported")
+    sp4, gl4 = b.observe(fmt="f32", all_seats=True)
+    sp4, gl4 = sp4.cpu().numpy(), gl4.cpu().numpy()
+    for i, g in enumerate(games):
+        for o in range(4):
+            osp, ogl = g.observe(o)
+            assert np.array_equal(sp4[i, o].view(np.uint32), osp.view(np.uint32)), (i, o)
+            assert np.array_equal(gl4[i, o], ogl), (i, o)
+    b.close()
+
+
 def test_invalid_actions_leave_state(jq):
     b = jq.JunqiBatch(8, show_mode=2)
     b.reset(3)

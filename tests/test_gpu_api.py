@@ -197,6 +197,7 @@ def test_world_push_state_step_and_legal(jq):
     for k in ("cell", "ptype", "pos", "zero", "move_count", "death_step", "turn", "move_counter", "mslc",
               "seat_dead", "flag_rev", "terminated", "zobrist", "hist_list"):
         G.compare_state({k: dev[k]}, {k: orc[k]}, ctx=f"push_state_from_envs {k}")
+
     for ply in range(25):
         seats = w.state.field_tensor("turn").cpu().numpy().astype(np.int8)
         offs, vals = w.legal_actions_csr(seats)
