@@ -410,6 +410,35 @@ def test_invalid_actions_leave_state(jq):
     for k in before:
         if k != "hist_list":
             assert np.array_equal(before[k], after[k]), k
+    # the same with the legal sets current (the step then tests membership in
+    # them): another seat's legal move, a destination the piece cannot reach,
+    # a move of a flag or mine
+    b.legal()
+    games = G.oracle_games_from_lineups(jq.generate_lineups(3, 8), 2)
+    rng = np.random.default_rng(5)
+    for kind in range(3):
+        acts = np.full(8, -1, np.int32)
+        for i, g in enumerate(games):
+            seat = int(g.turn)
+            if kind == 0:
+                acts[i] = rng.choice(g.legal_ids((seat + 1) % 4))
+            elif kind == 1:
+                ids = g.legal_ids(seat)
+                src = int(ids[0]) // 289
+                own = set(int(x) % 289 for x in ids if int(x) // 289 == src)
+                acts[i] = src * 289 + next(d for d in range(289) if d not in own and d != src)
+            else:
+                pid = next(p for p in range(seat * 30, seat * 30 + 30) if g.ptype[p] in (2, 3) and g.alive[p])
+                f = int(g.pos_y[pid]) * 17 + int(g.pos_x[pid])
+                acts[i] = f * 289 + (f + 1 if f % 17 < 16 else f - 1)
+        out = b.step(torch.from_numpy(acts).to(b.device))
+        assert not out["valid"].any(), kind
+        after = G.device_fields(b)
+        for k in before:
+            if k != "hist_list":
+                assert np.array_equal(before[k], after[k]), (kind, k)
+    ok = np.array([g.legal_ids()[0] for g in games], np.int32)
+    assert b.step(torch.from_numpy(ok).to(b.device))["valid"].all()
     b.close()
 
 
