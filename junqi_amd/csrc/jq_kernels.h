@@ -1017,6 +1017,8 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
                            int32_t *__restrict__ mask_words, uint8_t *__restrict__ mask_bool)
 {
     const int team = seat & 1;
+    __shared__ uint64_t srcset[3];   // compact source cells of the movable pieces
+    if (l < 3) srcset[l] = 0;
     BB occ, ea;
     env_boards(cell, team, occ, ea);
     // lanes p and p + 32 share piece p (p < 30), one half of its moves each
@@ -1066,12 +1068,16 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
     }
     const bool lead = mov && h == 0;   // the lane that reports piece p
     const int cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
-    // rank of this piece's source cell among the movable pieces
+    // rank of this piece's source cell among the movable pieces: the movable
+    // sources below it in a 129-bit set (compact order is flat order)
+    const int sc = mov ? flat_rank(cT.onm, src) : 0;
+    if (lead) atomicOr(reinterpret_cast<unsigned long long *>(&srcset[sc >> 6]), 1ull << (sc & 63));
+    __syncthreads();
     int rank = 0;
-    for (int j = 0; j < 30; ++j) {
-        const int oj = __shfl(src, j);
-        const bool mj = __shfl((int)mov, j) != 0;
-        rank += (mov && mj && oj < src) ? 1 : 0;
+    if (lead) {
+        const int w = sc >> 6;
+        rank = __popcll(srcset[w] & ((1ull << (sc & 63)) - 1)) + (w > 0 ? __popcll(srcset[0]) : 0) +
+               (w > 1 ? __popcll(srcset[1]) : 0);
     }
     const int nmov = __popcll(__ballot(lead));
     const int total = wave_sum(lead ? cnt : 0);
@@ -1083,7 +1089,7 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
     // canonical compact mask bits (gpu_rollout.py:1220-1238 layout): the two
     // lanes of a piece take alternate destination bits
     if (mov && (mask_words || mask_bool)) {
-        const int cs = rotl[flat_rank(cT.onm, src)] * NONB;
+        const int cs = rotl[sc] * NONB;
         const uint64_t half = h ? 0xAAAAAAAAAAAAAAAAull : 0x5555555555555555ull;
         uint64_t w[3] = {m0 & half, m1 & half, m2 & half};
         for (int q = 0; q < 3; ++q) {
