@@ -1406,7 +1406,7 @@ __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_
 // the legal sets of the next acting seat (k_legal with the current
 // turn), on the board the wave keeps in LDS, with no global round trip between
 // the three.
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_env_step(State S, const int32_t *__restrict__ actions, uint64_t sample_seed,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7, 8))) void k_env_step(State S, const int32_t *__restrict__ actions, uint64_t sample_seed,
                                                  uint64_t ply, const int32_t *__restrict__ offsets,
                                                  const int32_t *__restrict__ values, int32_t *__restrict__ actions_out,
                                                  StepOut O, int do_reset, int64_t reset_seed,
