@@ -141,6 +141,17 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Barrier of one wave working alone on its env (the whole block of a 64-thread
+// kernel, or one wave of a larger block): orders the wave's LDS and global
+// accesses like __syncthreads() without an s_barrier, so the other waves of a
+// larger block neither wait for it nor count it.
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 __device__ __forceinline__ size_t cm_idx(int env, int o, int pid) { return ((size_t)env * 4 + o) * PID_STRIDE + pid; }
 __device__ __forceinline__ size_t pc_idx(int env, int pid) { return (size_t)env * PID_STRIDE + pid; }
 

@@ -474,14 +474,14 @@ __device__ void kill_piece(const State &S, int env, int8_t *cell, int16_t *pos, 
     const int cur = pos[pid];
     if ((unsigned)cur >= (unsigned)NC) return;
     zob ^= zp(S.ztab, pid, ptype[pid], cur);
-    __syncthreads();
+    wave_sync();
     if (lane_id() == 0) {
         cell[cur] = -1; pos[pid] = -1;
         PieceRec &r = S.piece[pc_idx(env, pid)];
         r.pos = -1; r.dreason = (int8_t)reason; r.dstep = (int16_t)step; r.dloc = (int16_t)loc;
         S.cell[(size_t)env * CELL_STRIDE + cur] = -1;
     }
-    __syncthreads();
+    wave_sync();
 }
 
 __device__ void move_piece(const State &S, int env, int8_t *cell, int16_t *pos, const int8_t *ptype, int pid,
@@ -489,14 +489,14 @@ __device__ void move_piece(const State &S, int env, int8_t *cell, int16_t *pos, 
 {   // state.py:1005-1025
     const int t = ptype[pid];
     zob ^= zp(S.ztab, pid, t, src) ^ zp(S.ztab, pid, t, dst);
-    __syncthreads();
+    wave_sync();
     if (lane_id() == 0) {
         cell[src] = -1; cell[dst] = (int8_t)pid; pos[pid] = (int16_t)dst;
         S.cell[(size_t)env * CELL_STRIDE + src] = -1;
         S.cell[(size_t)env * CELL_STRIDE + dst] = (int8_t)pid;
         S.piece[pc_idx(env, pid)].pos = (int16_t)dst;
     }
-    __syncthreads();
+    wave_sync();
 }
 
 // Remove every live piece of `seat` (state.py:1639-1692): KILLED_BY_ENEMY at the
@@ -506,7 +506,7 @@ __device__ void purge_seat(const State &S, int env, int8_t *cell, int16_t *pos, 
 {
     const int l = lane_id();
     uint64_t z = 0;
-    __syncthreads();
+    wave_sync();
     if (l < 30) {
         const int pid = seat * 30 + l;
         const int cur = pos[pid];
@@ -519,7 +519,7 @@ __device__ void purge_seat(const State &S, int env, int8_t *cell, int16_t *pos, 
         }
     }
     zob ^= wave_xor(z);
-    __syncthreads();
+    wave_sync();
 }
 
 // CombatMemory update for EAT / KILLED (combat_memory.py:354-569). Lane o < 4
@@ -683,7 +683,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     if (acting && acting[env] != seat) return;
     const uint8_t sdead0 = E.sdead;
     if ((sdead0 >> seat) & 1) return;
-    __syncthreads();
+    wave_sync();
     if (!legal_pair(cell, ptype, seat, src, dst)) return;
 
     const int mc0 = E.mc, mslc0 = E.mslc;
@@ -871,7 +871,7 @@ __device__ void init_env(const State &S, int env, const int8_t *types, int8_t *l
         cell[f] = -1;
         if (lcell) lcell[f] = -1;
     }
-    __syncthreads();
+    wave_sync();
     uint64_t z = 0;
     for (int p = l; p < PID_STRIDE; p += 64) {
         const size_t pi = (size_t)env * PID_STRIDE + p;
@@ -1012,12 +1012,13 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
 // (cell, padded to CELL_STRIDE with -1), bits cleared and, for the canonical
 // mask, rotl filled. Piece positions / types come from the LDS arrays lpos /
 // ltype when given, else from the piece records.
+// srcset: 3 words of the wave's LDS for the compact source cells of the movable
+// pieces.
 __device__ __forceinline__ void legal_body(const State &S, int env, int l, int seat, bool off, const int8_t *cell, uint32_t *bits,
-                           const uint8_t *rotl, const int16_t *lpos, const int8_t *ltype, int32_t *__restrict__ counts,
-                           int32_t *__restrict__ mask_words, uint8_t *__restrict__ mask_bool)
+                           const uint8_t *rotl, const int16_t *lpos, const int8_t *ltype, uint64_t *srcset,
+                           int32_t *__restrict__ counts, int32_t *__restrict__ mask_words, uint8_t *__restrict__ mask_bool)
 {
     const int team = seat & 1;
-    __shared__ uint64_t srcset[3];   // compact source cells of the movable pieces
     if (l < 3) srcset[l] = 0;
     BB occ, ea;
     env_boards(cell, team, occ, ea);
@@ -1072,7 +1073,7 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
     // sources below it in a 129-bit set (compact order is flat order)
     const int sc = mov ? flat_rank(cT.onm, src) : 0;
     if (lead) atomicOr(reinterpret_cast<unsigned long long *>(&srcset[sc >> 6]), 1ull << (sc & 63));
-    __syncthreads();
+    wave_sync();
     int rank = 0;
     if (lead) {
         const int w = sc >> 6;
@@ -1107,7 +1108,7 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
         S.lg[env].seat = seat;
         if (counts) counts[env] = total;
     }
-    __syncthreads();
+    wave_sync();
     if (mask_words)
         for (int w = l; w < JQ_MASK_WORDS; w += 64) mask_words[(size_t)env * JQ_MASK_WORDS + w] = (int32_t)bits[w];
     if (mask_bool) {
@@ -1142,6 +1143,7 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     __shared__ int8_t cell[CELL_STRIDE];
     __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
     __shared__ uint8_t rotl[NONB + 3];   // world compact -> canonical compact of the acting seat
+    __shared__ uint64_t srcset[3];
     const EnvRec &E = S.env[env];
     const int seat = acting ? acting[env] : E.turn;
     const bool off = E.term || seat < 0 || seat > 3 || ((E.sdead >> (seat & 3)) & 1);
@@ -1152,7 +1154,7 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
         for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[s4][c];
     }
     __syncthreads();
-    legal_body(S, env, l, seat, off, cell, bits, rotl, nullptr, nullptr, counts, mask_words, mask_bool);
+    legal_body(S, env, l, seat, off, cell, bits, rotl, nullptr, nullptr, srcset, counts, mask_words, mask_bool);
 }
 
 // Exclusive scan of counts into offsets (N+1); one 1024-thread block walks the
@@ -1406,35 +1408,59 @@ __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_
 // the legal sets of the next acting seat (k_legal with the current
 // turn), on the board the wave keeps in LDS, with no global round trip between
 // the three.
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7, 8))) void k_env_step(State S, const int32_t *__restrict__ actions, uint64_t sample_seed,
-                                                 uint64_t ply, const int32_t *__restrict__ offsets,
-                                                 const int32_t *__restrict__ values, int32_t *__restrict__ actions_out,
-                                                 StepOut O, int do_reset, int64_t reset_seed,
-                                                 int32_t *__restrict__ counts, int32_t *__restrict__ mask_words)
+// One wave's board while it steps its env: the LDS that step_env, init_env and
+// legal_body work on.
+struct EnvLds {
+    alignas(16) uint32_t bits[JQ_MASK_WORDS_PAD];
+    uint64_t srcset[3];
+    int16_t pos[PID_STRIDE];
+    int8_t ptype[PID_STRIDE];
+    int8_t cell[CELL_STRIDE];
+    uint8_t rotl[NONB + 3];
+};
+
+// Inputs of one env-step beyond the state: the action source (`actions`, else a
+// Philox pick from the env's previous CSR row `offsets` / `values` with
+// `counts`), the pool restart and the outputs.
+struct EnvStepArgs {
+    const int32_t *actions; uint64_t sample_seed, ply; const int32_t *offsets, *values;
+    int32_t *actions_out; StepOut O; int do_reset; int64_t reset_seed;
+    int32_t *counts, *mask_words;
+};
+
+// The env-step of `env` by one wave (lane l): sample its action, apply the ply,
+// restart the env from the setup pool if it ended, then the next seat's legal
+// sets and canonical mask, all on the board the wave keeps in E. Only wave-level
+// barriers: the waves of a larger block run it on different envs.
+__device__ __forceinline__ void env_step_wave(const State &S, int env, int l, const EnvStepArgs &A, EnvLds &E)
 {
-    const int env = blockIdx.x, l = threadIdx.x;
-    if (env >= S.n) return;
-    const int32_t a = actions ? actions[env] : sample_pick(env, counts, offsets, values, sample_seed, ply);
-    if (actions_out && l == 0) actions_out[env] = a;
-    __shared__ int8_t cell[CELL_STRIDE];
-    __shared__ int16_t pos[PID_STRIDE];
-    __shared__ int8_t ptype[PID_STRIDE];
-    __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
-    __shared__ uint8_t rotl[NONB + 3];
+    const int32_t a = A.actions ? A.actions[env]
+                                : sample_pick(env, A.counts, A.offsets, A.values, A.sample_seed, A.ply);
+    if (A.actions_out && l == 0) A.actions_out[env] = a;
     TurnAfter nx;
-    step_env(S, env, l, a, nullptr, 0, O, cell, pos, ptype, nx);
-    __syncthreads();
-    if (do_reset && S.pool_size > 0 && nx.term) {
-        init_env(S, env, S.pool + (size_t)reset_pool_index(env, reset_seed, S.pool_size) * NP, cell, pos, ptype);
+    step_env(S, env, l, a, nullptr, 0, A.O, E.cell, E.pos, E.ptype, nx);
+    wave_sync();
+    if (A.do_reset && S.pool_size > 0 && nx.term) {
+        init_env(S, env, S.pool + (size_t)reset_pool_index(env, A.reset_seed, S.pool_size) * NP, E.cell, E.pos,
+                 E.ptype);
         nx.turn = 0; nx.term = false; nx.sdead = 0;
     }
     const int seat = nx.turn;
     const bool off = nx.term || seat < 0 || seat > 3 || ((nx.sdead >> (seat & 3)) & 1);
-    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
-    if (mask_words)
-        for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[seat & 3][c];
-    __syncthreads();
-    legal_body(S, env, l, seat, off, cell, bits, rotl, pos, ptype, counts, mask_words, nullptr);
+    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) E.bits[w] = 0;
+    if (A.mask_words)
+        for (int c = l; c < NONB; c += 64) E.rotl[c] = cT.rotc[seat & 3][c];
+    wave_sync();
+    legal_body(S, env, l, seat, off, E.cell, E.bits, E.rotl, E.pos, E.ptype, E.srcset, A.counts, A.mask_words,
+               nullptr);
+}
+
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7, 8))) void k_env_step(State S, EnvStepArgs A)
+{
+    const int env = blockIdx.x;
+    if (env >= S.n) return;
+    __shared__ EnvLds E;
+    env_step_wave(S, env, threadIdx.x, A, E);
 }
 
 

@@ -528,13 +528,15 @@ int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_
     if (rc) return rc;
     if (!counts || !offsets || !values) return fail(JQ_E_ARG, "env_step needs counts, offsets and values");
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before stepping");
-    StepOut O = {};
-    O.term = terminated;
-    O.reward = reward;
+    if (spatial && (obs_fmt < JQ_OBS_F32 || obs_fmt > JQ_OBS_U8))
+        return fail(JQ_E_ARG, "bad observation format %d", obs_fmt);
+    EnvStepArgs A = {};
+    A.actions = actions; A.sample_seed = sample_seed; A.ply = ply; A.offsets = offsets; A.values = values;
+    A.actions_out = actions_out; A.O.term = terminated; A.O.reward = reward;
+    A.do_reset = e->S.pool ? 1 : 0; A.reset_seed = reset_seed; A.counts = counts; A.mask_words = mask_words;
     // sample (unless actions are given), ply, restart from the pool and the
     // next seat's legal sets in one kernel
-    hipLaunchKernelGGL(k_env_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, actions, sample_seed, ply,
-                       offsets, values, actions_out, O, e->S.pool ? 1 : 0, reset_seed, counts, mask_words);
+    hipLaunchKernelGGL(k_env_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, A);
     if ((rc = launch_check("k_env_step")) != 0) return rc;
     hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, strm(stream), counts, offsets, e->S.n);
     if ((rc = launch_check("k_scan")) != 0) return rc;

@@ -442,20 +442,21 @@ def test_invalid_actions_leave_state(jq):
     b.close()
 
 
-@pytest.mark.parametrize("max_moves,plies", [(4000, 120), (25, 90)])
-def test_env_step_fused_matches_oracle(jq, max_moves, plies):
-    """The fused env-step (sample, step, auto-reset, legal, u8 obs) agrees with
+@pytest.mark.parametrize("max_moves,plies,n,fmt", [(4000, 120, 64, "u8"), (25, 90, 62, "u8"), (25, 40, 33, "f32")])
+def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt):
+    """The env-step (sample, step, auto-reset, legal, observation) agrees with
     the oracle stepped with the same Philox choices: state, sorted CSR rows,
     canonical mask words and observations after every step. A 25-move cap
-    makes games end and restart from the pool every 25 plies."""
-    n = 64
-    print(f"[env_step] max_moves={max_moves} plies={plies}", flush=True)
+    makes games end and restart from the pool every 25 plies. Odd batch
+    sizes and both the u8 and the f32 observation."""
+    print(f"[env_step] max_moves={max_moves} plies={plies} n={n} fmt={fmt}", flush=True)
     b = jq.JunqiBatch(n, show_mode=2, pool_size=128, max_num_moves=max_moves)
     b.reset(21)
     games = G.oracle_games_from_lineups(jq.generate_lineups(21, n), 2, max_moves)
     b.legal()
-    sp = torch.empty((n, 317, 17, 17), dtype=torch.uint8, device=b.device)
-    aux = torch.empty((n, 6, 17, 17), dtype=torch.float32, device=b.device)
+    u8 = fmt == "u8"
+    sp = torch.empty((n, 317, 17, 17), dtype=torch.uint8 if u8 else torch.float32, device=b.device)
+    aux = torch.empty((n, 6, 17, 17), dtype=torch.float32, device=b.device) if u8 else None
     gl = torch.empty((n, 28), dtype=torch.float32, device=b.device)
     term = torch.empty(n, dtype=torch.uint8, device=b.device)
     rew = torch.empty(n, dtype=torch.float32, device=b.device)
@@ -465,7 +466,7 @@ def test_env_step_fused_matches_oracle(jq, max_moves, plies):
     resets = 0
     for ply in range(plies):
         offs = b.offsets.cpu().numpy(); vals = b.values.cpu().numpy(); counts = b.counts.cpu().numpy()
-        b.env_step(sample_seed=77, ply=ply, reset_seed=ply, obs_fmt="u8", spatial=sp, aux=aux, glob=gl,
+        b.env_step(sample_seed=77, ply=ply, reset_seed=ply, obs_fmt=fmt, spatial=sp, aux=aux, glob=gl,
                    terminated=term, reward=rew, actions_out=acts)
         a = acts.cpu().numpy()
         tm = term.cpu().numpy()
@@ -483,15 +484,18 @@ def test_env_step_fused_matches_oracle(jq, max_moves, plies):
                                   max_num_moves=max_moves)
         G.compare_state(G.device_fields(b), G.oracle_fields(games), ctx=f"fused ply {ply}")
         offs = b.offsets.cpu().numpy(); vals = b.values.cpu().numpy(); mw = b.mask_words.cpu().numpy()
-        u8 = sp.cpu().numpy(); ax = aux.cpu().numpy(); g2 = gl.cpu().numpy()
+        spn = sp.cpu().numpy(); ax = aux.cpu().numpy() if u8 else None; g2 = gl.cpu().numpy()
         for i, g in enumerate(games):
             ids = g.legal_ids()
             assert np.array_equal(vals[offs[i]:offs[i + 1]], ids), (ply, i)
             assert np.array_equal(mw[i], G.canonical_mask_words(ids, int(g.turn), tables)), (ply, i)
             osp, ogl = g.observe(int(g.turn))
-            d = dec[u8[i]]
-            for j, ch in enumerate(jq.AUX_CHANNELS):
-                d[ch] = ax[i, j]
+            if u8:
+                d = dec[spn[i]]
+                for j, ch in enumerate(jq.AUX_CHANNELS):
+                    d[ch] = ax[i, j]
+            else:
+                d = spn[i]
             assert np.array_equal(d.view(np.uint32), osp.view(np.uint32)), (ply, i)
             assert np.array_equal(g2[i], ogl)
     if max_moves < 100:
