@@ -24,6 +24,7 @@ __constant__ Tables cT;
 __constant__ uint8_t cBVAL[BC_COUNT][12];   // belief code x type -> obs value code
 __constant__ float cDECODE[256];             // obs value code -> float
 constexpr int JQ_MASK_WORDS_PAD = 528;
+constexpr int LSCR_WORDS = 12;   // legal_body's per-wave LDS scratch (u64 words)
 
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
@@ -72,8 +73,12 @@ __device__ __forceinline__ int wave_sum(int v)
 
 // Reachability closure of an engineer standing on rail index `src_r`: the source
 // plus every rail node joined to it through empty rail cells. Lane l evaluates
-// nodes l and l+64 each hop; the frontier grows until a hop adds nothing.
-__device__ void rail_closure(const int8_t *cell, int src_r, uint64_t &r0, uint64_t &r1)
+// nodes l and l+64 each hop; the frontier grows until a hop adds nothing, or
+// until it touches a node of the target set (t0, t1) when one is given. A node
+// already in the closure may be reported again by its lane: growth is what the
+// ballot adds beyond the closure.
+__device__ void rail_closure(const int8_t *cell, int src_r, uint64_t &r0, uint64_t &r1, uint64_t t0 = 0,
+                             uint64_t t1 = 0)
 {
     const int l = lane_id();
     const int v1 = l + 64;
@@ -84,12 +89,12 @@ __device__ void rail_closure(const int8_t *cell, int src_r, uint64_t &r0, uint64
     r0 = src_r < 64 ? (1ull << src_r) : 0ull;
     r1 = src_r >= 64 ? (1ull << (src_r - 64)) : 0ull;
     for (int hop = 0; hop < NRAIL; ++hop) {
-        const bool n0 = e0 && !((r0 >> l) & 1) && (((a0 & r0) | (a1 & r1)) != 0);
-        const bool n1 = e1 && !((r1 >> (v1 & 63)) & 1) && (((b0 & r0) | (b1 & r1)) != 0);
-        const uint64_t g0 = __ballot(n0), g1 = __ballot(n1);
-        if (!(g0 | g1)) break;
+        if ((r0 & t0) | (r1 & t1)) break;
+        const uint64_t g0 = __ballot(e0 && ((a0 & r0) | (a1 & r1)) != 0);
+        const uint64_t g1 = __ballot(e1 && ((b0 & r0) | (b1 & r1)) != 0) & 0x1FFull;
+        if (!((g0 & ~r0) | (g1 & ~r1))) break;
         r0 |= g0;
-        r1 |= g1 & 0x1FFull;
+        r1 |= g1;
     }
 }
 
@@ -251,11 +256,12 @@ __device__ __forceinline__ BB piece_moves_half(int sc, int r, bool engineer, int
     return m;
 }
 
-// Rail destinations of up to three engineers at once (move_gen.py:870-895):
-// lane j < ne gets, in m, the landable rail nodes adjacent to the closure of
-// engineer j's source (rail index sr, held by lane j) through empty rail
-// nodes. Lane v evaluates rail nodes v and v + 64 each hop.
-__device__ __forceinline__ void engineers_bb(int ne, const int sr[3], const BB &occ, const BB &ea, BB out[3])
+// Rail destinations of up to three engineers at once (move_gen.py:870-895): the
+// landable rail nodes adjacent to the closure of engineer j's source (rail
+// index sr[j]) through empty rail nodes, OR-ed into the wave's LDS words
+// dst[3j .. 3j + 2] (compact cells; zero on entry). Lane v evaluates rail nodes
+// v and v + 64 each hop; an engineer whose closure stopped growing is skipped.
+__device__ __forceinline__ void engineers_bb(int ne, const int sr[3], const BB &occ, const BB &ea, uint64_t *dst)
 {
     const int l = lane_id(), v1 = l + 64;
     const bool has1 = v1 < NRAIL;
@@ -265,32 +271,31 @@ __device__ __forceinline__ void engineers_bb(int ne, const int sr[3], const BB &
     const uint64_t a0 = cT.rnbr[l][0], a1 = cT.rnbr[l][1];
     const uint64_t b0 = has1 ? cT.rnbr[v1][0] : 0ull, b1 = has1 ? cT.rnbr[v1][1] : 0ull;
     uint64_t r0[3], r1[3];
+    bool grow[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
+        grow[j] = j < ne;
         r0[j] = j < ne && sr[j] < 64 ? 1ull << sr[j] : 0ull;
         r1[j] = j < ne && sr[j] >= 64 ? 1ull << (sr[j] - 64) : 0ull;
     }
-    for (int hop = 0; hop < NRAIL; ++hop) {
-        uint64_t grew = 0;
+    for (int hop = 0; hop < NRAIL && (grow[0] || grow[1] || grow[2]); ++hop) {
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-            const bool n0 = e0 && !((r0[j] >> l) & 1) && (((a0 & r0[j]) | (a1 & r1[j])) != 0);
-            const bool n1 = e1 && !((r1[j] >> (v1 & 63)) & 1) && (((b0 & r0[j]) | (b1 & r1[j])) != 0);
-            const uint64_t g0 = __ballot(n0), g1 = __ballot(n1) & 0x1FFull;
+            if (!grow[j]) continue;
+            const uint64_t g0 = __ballot(e0 && ((a0 & r0[j]) | (a1 & r1[j])) != 0);
+            const uint64_t g1 = __ballot(e1 && ((b0 & r0[j]) | (b1 & r1[j])) != 0) & 0x1FFull;
+            grow[j] = ((g0 & ~r0[j]) | (g1 & ~r1[j])) != 0;
             r0[j] |= g0;
             r1[j] |= g1;
-            grew |= g0 | g1;
         }
-        if (!grew) break;
     }
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-        BB p = {0, 0, 0};
-        const bool d0 = l != sr[j] && l0 && (((a0 & r0[j]) | (a1 & r1[j])) != 0);
-        const bool d1 = has1 && v1 != sr[j] && l1 && (((b0 & r0[j]) | (b1 & r1[j])) != 0);
-        if (d0) setbit3(p.w0, p.w1, p.w2, c0);
-        if (d1) setbit3(p.w0, p.w1, p.w2, c1);
-        out[j] = {wave_or(p.w0), wave_or(p.w1), wave_or(p.w2)};
+        if (j >= ne) break;
+        if (l != sr[j] && l0 && ((a0 & r0[j]) | (a1 & r1[j])) != 0)
+            atomicOr(reinterpret_cast<unsigned long long *>(&dst[3 * j + (c0 >> 6)]), 1ull << (c0 & 63));
+        if (has1 && v1 != sr[j] && l1 && ((b0 & r0[j]) | (b1 & r1[j])) != 0)
+            atomicOr(reinterpret_cast<unsigned long long *>(&dst[3 * j + (c1 >> 6)]), 1ull << (c1 & 63));
     }
 }
 
@@ -350,12 +355,13 @@ __device__ __forceinline__ bool run_clear(const int8_t *cell, int src, int dst, 
 }
 
 __device__ __forceinline__ bool engineer_reaches(const int8_t *cell, int src, int dst)
-{   // move_gen.py:186-224
+{   // move_gen.py:186-224: dst is adjacent to the closure of src
     if (!is_rail(src) || !is_rail(dst) || src == dst) return false;
     uint64_t r0, r1;
-    rail_closure(cell, cT.railidx[src], r0, r1);
     const int dr = cT.railidx[dst];
-    return ((cT.rnbr[dr][0] & r0) | (cT.rnbr[dr][1] & r1)) != 0;
+    const uint64_t t0 = cT.rnbr[dr][0], t1 = cT.rnbr[dr][1];
+    rail_closure(cell, cT.railidx[src], r0, r1, t0, t1);
+    return ((t0 & r0) | (t1 & r1)) != 0;
 }
 
 // is_legal_move (move_gen.py:299-376), uniform over the wave.
@@ -1012,13 +1018,14 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
 // (cell, padded to CELL_STRIDE with -1), bits cleared and, for the canonical
 // mask, rotl filled. Piece positions / types come from the LDS arrays lpos /
 // ltype when given, else from the piece records.
-// srcset: 3 words of the wave's LDS for the compact source cells of the movable
-// pieces.
+// lscr: LSCR_WORDS words of the wave's LDS, the compact source cells of the
+// movable pieces (words 0-2) and the engineers' rail destinations (3-11).
 __device__ __forceinline__ void legal_body(const State &S, int env, int l, int seat, bool off, const int8_t *cell, uint32_t *bits,
-                           const uint8_t *rotl, const int16_t *lpos, const int8_t *ltype, uint64_t *srcset,
+                           const uint8_t *rotl, const int16_t *lpos, const int8_t *ltype, uint64_t *lscr,
                            int32_t *__restrict__ counts, int32_t *__restrict__ mask_words, uint8_t *__restrict__ mask_bool)
 {
     const int team = seat & 1;
+    uint64_t *srcset = lscr, *edst = lscr + 3;
     if (l < 3) srcset[l] = 0;
     BB occ, ea;
     env_boards(cell, team, occ, ea);
@@ -1061,11 +1068,13 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
             engs &= engs - 1;
             sr[j] = lanes[j] < 64 ? __shfl(ridx, lanes[j]) : -1;
         }
-        BB em[3];
-        engineers_bb(ne, sr, occ, ea, em);
+        if (l < 9) edst[l] = 0;
+        engineers_bb(ne, sr, occ, ea, edst);
+        wave_sync();
 #pragma unroll
         for (int j = 0; j < 3; ++j)
-            if (p == lanes[j]) { m0 |= em[j].w0; m1 |= em[j].w1; m2 |= em[j].w2; }
+            if (p == lanes[j]) { m0 |= edst[3 * j]; m1 |= edst[3 * j + 1]; m2 |= edst[3 * j + 2]; }
+        wave_sync();
     }
     const bool lead = mov && h == 0;   // the lane that reports piece p
     const int cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
@@ -1143,7 +1152,7 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     __shared__ int8_t cell[CELL_STRIDE];
     __shared__ uint32_t bits[JQ_MASK_WORDS_PAD];
     __shared__ uint8_t rotl[NONB + 3];   // world compact -> canonical compact of the acting seat
-    __shared__ uint64_t srcset[3];
+    __shared__ uint64_t lscr[LSCR_WORDS];
     const EnvRec &E = S.env[env];
     const int seat = acting ? acting[env] : E.turn;
     const bool off = E.term || seat < 0 || seat > 3 || ((E.sdead >> (seat & 3)) & 1);
@@ -1154,7 +1163,7 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
         for (int c = l; c < NONB; c += 64) rotl[c] = cT.rotc[s4][c];
     }
     __syncthreads();
-    legal_body(S, env, l, seat, off, cell, bits, rotl, nullptr, nullptr, srcset, counts, mask_words, mask_bool);
+    legal_body(S, env, l, seat, off, cell, bits, rotl, nullptr, nullptr, lscr, counts, mask_words, mask_bool);
 }
 
 // Exclusive scan of counts into offsets (N+1); one 1024-thread block walks the
@@ -1412,7 +1421,7 @@ __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_
 // legal_body work on.
 struct EnvLds {
     alignas(16) uint32_t bits[JQ_MASK_WORDS_PAD];
-    uint64_t srcset[3];
+    uint64_t lscr[LSCR_WORDS];
     int16_t pos[PID_STRIDE];
     int8_t ptype[PID_STRIDE];
     int8_t cell[CELL_STRIDE];
@@ -1451,7 +1460,7 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
     if (A.mask_words)
         for (int c = l; c < NONB; c += 64) E.rotl[c] = cT.rotc[seat & 3][c];
     wave_sync();
-    legal_body(S, env, l, seat, off, E.cell, E.bits, E.rotl, E.pos, E.ptype, E.srcset, A.counts, A.mask_words,
+    legal_body(S, env, l, seat, off, E.cell, E.bits, E.rotl, E.pos, E.ptype, E.lscr, A.counts, A.mask_words,
                nullptr);
 }
 
