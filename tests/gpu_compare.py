@@ -149,5 +149,20 @@ def philox_first_word(c0: int, c1: int, c2: int, c3: int, k0: int, k1: int) -> i
     return c0
 
 
+def philox_first_word_np(c0: np.ndarray, c1: int, c2: int, c3: int, k0: int, k1: int) -> np.ndarray:
+    """philox_first_word over an array of first counter words."""
+    M = np.uint64(0xFFFFFFFF)
+    c0 = np.asarray(c0, dtype=np.uint64)
+    c1, c2, c3 = (np.full(c0.shape, v, dtype=np.uint64) for v in (c1, c2, c3))
+    k0, k1 = np.uint64(k0), np.uint64(k1)
+    for _ in range(10):
+        p0 = np.uint64(0xD2511F53) * c0
+        p1 = np.uint64(0xCD9E8D57) * c2
+        c0, c1, c2, c3 = ((p1 >> np.uint64(32)) ^ c1 ^ k0) & M, p1 & M, ((p0 >> np.uint64(32)) ^ c3 ^ k1) & M, p0 & M
+        k0 = (k0 + np.uint64(0x9E3779B9)) & M
+        k1 = (k1 + np.uint64(0xBB67AE85)) & M
+    return c0
+
+
 def oracle_games_from_lineups(lineups: np.ndarray, show_mode: int, max_num_moves: int = 4000) -> list:
     return [O.Game(lu, show_mode=show_mode, max_num_moves=max_num_moves) for lu in lineups]
