@@ -9,6 +9,10 @@
  * (paths relative to the reference repository). Semantic authority is
  * junqi_core/state.py::GameState (not BatchedGameState, whose divergences are
  * documented in DESIGN.md).
+ *
+ * Parity unpinned (jqo_observe): DARK-mode teammate belief values after the
+ * first ply beyond the probability-vector invariants the tests check, and
+ * combat-memory / belief values beyond step 100 of the reference's hashed games.
  */
 #ifndef JQ_ORACLE_H
 #define JQ_ORACLE_H

@@ -599,3 +599,49 @@ def test_slot_mask_empty_for_dead_seat_and_finished_game():
     assert not g.legal_slots(1).any()   # no pieces
     g.buf[0]["terminated"] = 1
     assert not g.legal_slots(0).any()
+
+
+def _sorted_rows(m: np.ndarray) -> list:
+    return sorted(map(tuple, np.asarray(m, dtype=np.float64).round(7)))
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_dark_observation_relations(seed):
+    """DARK hides only the teammate's piece types from an observer
+    (info_model.py:568-577) and adds the dark_teammate plane
+    (observation.py:683-697). With one setup and one move sequence, DARK and
+    HALF_DARK observations of all four observers are equal at every ply except
+    on prob_teammate (12-23) and dark_teammate (24); DARK's plane 24 is the
+    teammate occupancy that HALF_DARK's one-hot planes 12-23 sum to (zero in
+    HALF_DARK); DARK's teammate rows are probability vectors on those cells and
+    zero elsewhere; at ply 0 they are the per-slot priors, the same multiset as
+    the enemy rows of HALF_DARK's belief planes 27-38 / 39-50 (masks 25 / 26),
+    which the reference's observation hashes pin."""
+    setup = O.random_setup(700 + seed)
+    hd, dk = O.Game(setup, show_mode=2), O.Game(setup, show_mode=1)
+    rng = np.random.default_rng(seed)
+    other = np.r_[0:12, 25:317]
+    for ply in range(160):
+        for o in range(4):
+            sh, gh = hd.observe(o)
+            sd, gd = dk.observe(o)
+            sh, sd = sh.reshape(317, 289), sd.reshape(317, 289)
+            assert np.array_equal(sh[other], sd[other]), (ply, o)
+            assert np.array_equal(gh, gd), (ply, o)
+            occ = sh[12:24].sum(0)
+            assert set(np.unique(occ)) <= {0.0, 1.0}
+            assert not sh[24].any()
+            assert np.array_equal(sd[24], occ), (ply, o)
+            rows = sd[12:24][:, occ == 1]
+            assert (rows >= 0).all() and np.allclose(rows.sum(0), 1.0, atol=1e-5), (ply, o)
+            assert not sd[12:24][:, occ == 0].any(), (ply, o)
+            if ply == 0:
+                assert _sorted_rows(rows.T) == _sorted_rows(sh[27:39][:, sh[25] == 1].T)
+                assert _sorted_rows(rows.T) == _sorted_rows(sh[39:51][:, sh[26] == 1].T)
+        ids = hd.legal_ids()
+        if hd.terminated or not len(ids):
+            break
+        assert np.array_equal(ids, dk.legal_ids())
+        a = int(ids[rng.integers(len(ids))])
+        hd.step_id(a)
+        dk.step_id(a)
