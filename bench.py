@@ -120,8 +120,8 @@ def main() -> int:
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the environment shards by games with no exchange, "
-              "so runs with more than one GPU are not part of this build", file=sys.stderr)
+        print("bench.py measures one GPU: the environment shards by games with no exchange "
+              "(G GPUs = G independent batches), so it has no multi-GPU run", file=sys.stderr)
         return 2
     import numpy as np
     import torch

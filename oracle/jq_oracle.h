@@ -7,8 +7,8 @@
  *
  * Every function restates the behaviour of one reference function and cites it
  * (paths relative to the reference repository). Semantic authority is
- * junqi_core/state.py::GameState (not BatchedGameState, whose divergences are
- * documented in DESIGN.md).
+ * junqi_core/state.py::GameState; where BatchedGameState diverges from it,
+ * GameState's behaviour is the one restated.
  *
  * Parity unpinned (jqo_observe): DARK-mode teammate belief values after the
  * first ply beyond the probability-vector invariants the tests check, and
