@@ -1245,42 +1245,47 @@ __device__ __forceinline__ int select64(uint64_t x, int k)
 }
 
 // Write each env's ids at its offset: pieces in ascending source order, each
-// piece's destinations ascending (compact order = flat order). One wave per
-// env; lane j produces ids j, j + 64, ...: it finds its piece from the running
-// counts, the destination by selecting a bit of that piece's mask, and maps it
-// to a flat cell through an LDS copy of the compact table.
+// piece's destinations ascending (compact order = flat order). Two envs per
+// wave: half h (lanes 32h .. 32h + 31) takes env 2 * block + h, which fits since
+// a seat has at most 30 movable pieces. Lane j of a half produces ids j, j + 32,
+// ...: it finds its piece from the running counts, the destination by selecting
+// a bit of that piece's mask, and maps it to a flat cell through an LDS copy of
+// the compact table.
 __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict__ offsets, int32_t *__restrict__ values)
 {
-    const int env = blockIdx.x, l = threadIdx.x;
-    if (env >= S.n) return;
+    const int l = threadIdx.x, h = l >> 5, p = l & 31;
+    const int env = 2 * (int)blockIdx.x + h;
+    const bool live = env < S.n;
     __shared__ int16_t c2f[NONB + 3];
-    __shared__ int32_t start[33];     // first id of each piece, start[n] = total
+    __shared__ int32_t start[2][33];   // per half: first id of each piece, start[n] = total
     for (int c = l; c < NONB; c += 64) c2f[c] = cT.c2f[c];
-    const LegalRec &G = S.lg[env];
-    const int n = G.n;
+    const int n = live ? min((int)S.lg[env].n, 30) : 0;
     int cnt = 0, src = 0;
     uint64_t m0 = 0, m1 = 0, m2 = 0;
-    if (l < n) {
-        src = G.src[l];
-        m0 = G.mask[l][0]; m1 = G.mask[l][1]; m2 = G.mask[l][2];
+    if (p < n) {
+        const LegalRec &G = S.lg[env];
+        src = G.src[p];
+        m0 = G.mask[p][0]; m1 = G.mask[p][1]; m2 = G.mask[p][2];
         cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
     }
     int incl = cnt;
-    for (int o = 1; o < 64; o <<= 1) { const int v = __shfl_up(incl, o); if (l >= o) incl += v; }
-    if (l < n) start[l] = incl - cnt;
-    const int total = __shfl(incl, 63);
-    if (l == 0) start[n] = total;
-    const int base = offsets[env];
+    for (int o = 1; o < 32; o <<= 1) { const int v = __shfl_up(incl, o, 32); if (p >= o) incl += v; }
+    if (p < n) start[h][p] = incl - cnt;
+    const int total = __shfl(incl, 31, 32);
+    if (p == 0) start[h][n] = total;
+    const int base = live ? offsets[env] : 0;
     __syncthreads();
-    for (int b = 0; b < total; b += 64) {   // uniform trip count: every lane takes the shuffles
-        const int i = b + l;
+    // uniform trip count (the larger half's total): every lane takes the shuffles
+    const int trips = max(__shfl(total, 0), __shfl(total, 32));
+    for (int b = 0; b < trips; b += 32) {
+        const int i = b + p;
         int j = 0;   // piece of id i: the last piece whose start is <= i
         for (int step = 16; step >= 1; step >>= 1)
-            if (j + step < n && start[j + step] <= i) j += step;
-        const uint64_t w0 = __shfl(m0, j), w1 = __shfl(m1, j), w2 = __shfl(m2, j);
-        const int s = __shfl(src, j);
+            if (j + step < n && start[h][j + step] <= i) j += step;
+        const uint64_t w0 = __shfl(m0, j, 32), w1 = __shfl(m1, j, 32), w2 = __shfl(m2, j, 32);
+        const int s = __shfl(src, j, 32);
         if (i < total) {
-            const int k = i - start[j];
+            const int k = i - start[h][j];
             const int c0 = __popcll(w0), c1 = __popcll(w1);
             const int c = k < c0 ? select64(w0, k)
                                  : k < c0 + c1 ? 64 + select64(w1, k - c0) : 128 + select64(w2, k - c0 - c1);

@@ -416,7 +416,7 @@ int jq_legal(jq_env *e, const int8_t *acting, int32_t *counts, int32_t *offsets,
         if ((rc = launch_check("k_scan")) != 0) return rc;
     }
     if (values) {
-        hipLaunchKernelGGL(k_emit, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, offsets, values);
+        hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values);
         if ((rc = launch_check("k_emit")) != 0) return rc;
     }
     return JQ_OK;
@@ -540,7 +540,7 @@ int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_
     if ((rc = launch_check("k_env_step")) != 0) return rc;
     hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, strm(stream), counts, offsets, e->S.n);
     if ((rc = launch_check("k_scan")) != 0) return rc;
-    hipLaunchKernelGGL(k_emit, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, offsets, values);
+    hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values);
     if ((rc = launch_check("k_emit")) != 0) return rc;
     // sequential on purpose: the u8 observation grid holds every CU's LDS, so a
     // concurrent launch only slows both down
