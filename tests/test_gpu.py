@@ -442,14 +442,18 @@ def test_invalid_actions_leave_state(jq):
     b.close()
 
 
-@pytest.mark.parametrize("max_moves,plies,n,fmt", [(4000, 120, 64, "u8"), (25, 90, 62, "u8"), (25, 40, 33, "f32")])
-def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt):
+@pytest.mark.parametrize("max_moves,plies,n,fmt,given", [(4000, 120, 64, "u8", False), (25, 90, 62, "u8", False),
+                                                          (25, 40, 33, "f32", False), (25, 60, 40, "u8", True)])
+def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt, given):
     """The env-step (sample, step, auto-reset, legal, observation) agrees with
     the oracle stepped with the same Philox choices: state, sorted CSR rows,
     canonical mask words and observations after every step. A 25-move cap
     makes games end and restart from the pool every 25 plies. Odd batch
-    sizes and both the u8 and the f32 observation."""
-    print(f"[env_step] max_moves={max_moves} plies={plies} n={n} fmt={fmt}", flush=True)
+    sizes and both the u8 and the f32 observation. `given`: the caller passes
+    the actions instead, legal ones mixed with -1 and arbitrary (mostly
+    illegal) world ids, which leave their env as it was."""
+    print(f"[env_step] max_moves={max_moves} plies={plies} n={n} fmt={fmt} given={given}", flush=True)
+    rng = np.random.default_rng(n)
     b = jq.JunqiBatch(n, show_mode=2, pool_size=128, max_num_moves=max_moves)
     b.reset(21)
     games = G.oracle_games_from_lineups(jq.generate_lineups(21, n), 2, max_moves)
@@ -466,13 +470,26 @@ def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt):
     resets = 0
     for ply in range(plies):
         offs = b.offsets.cpu().numpy(); vals = b.values.cpu().numpy(); counts = b.counts.cpu().numpy()
-        b.env_step(sample_seed=77, ply=ply, reset_seed=ply, obs_fmt=fmt, spatial=sp, aux=aux, glob=gl,
+        chosen = None
+        if given:
+            chosen = np.full(n, -1, np.int32)
+            for i, g in enumerate(games):
+                r, ids = rng.random(), g.legal_ids()
+                if r < 0.15:
+                    chosen[i] = int(rng.integers(289 * 289))
+                elif r >= 0.25 and len(ids):
+                    chosen[i] = int(ids[rng.integers(len(ids))])
+        b.env_step(actions=None if chosen is None else torch.from_numpy(chosen).to(b.device),
+                   sample_seed=77, ply=ply, reset_seed=ply, obs_fmt=fmt, spatial=sp, aux=aux, glob=gl,
                    terminated=term, reward=rew, actions_out=acts)
         a = acts.cpu().numpy()
         tm = term.cpu().numpy()
         for i, g in enumerate(games):
-            u = G.philox_first_word(i, ply, 0, 0, 77, 0)
-            want = vals[offs[i] + ((u * int(counts[i])) >> 32)] if counts[i] else -1
+            if given:
+                want = chosen[i]
+            else:
+                u = G.philox_first_word(i, ply, 0, 0, 77, 0)
+                want = vals[offs[i] + ((u * int(counts[i])) >> 32)] if counts[i] else -1
             assert a[i] == want
             if want >= 0:
                 g.step_id(int(want))
