@@ -1444,8 +1444,8 @@ struct EnvStepArgs {
 
 // The env-step of `env` by one wave (lane l): sample its action, apply the ply,
 // restart the env from the setup pool if it ended, then the next seat's legal
-// sets and canonical mask, all on the board the wave keeps in E. Only wave-level
-// barriers: the waves of a larger block run it on different envs.
+// sets and canonical mask, all on the board the wave keeps in E. It synchronises
+// only its own wave (wave_sync), so it never waits on other waves of a block.
 __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, const EnvStepArgs &A, EnvLds &E)
 {
     const int32_t a = A.actions ? A.actions[env]
