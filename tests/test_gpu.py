@@ -442,21 +442,22 @@ def test_invalid_actions_leave_state(jq):
     b.close()
 
 
-@pytest.mark.parametrize("max_moves,plies,n,fmt,given", [(4000, 120, 64, "u8", False), (25, 90, 62, "u8", False),
-                                                          (25, 40, 33, "f32", False), (25, 60, 40, "u8", True)])
-def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt, given):
+@pytest.mark.parametrize("max_moves,plies,n,fmt,given,show", [
+    (4000, 120, 64, "u8", False, 2), (25, 90, 62, "u8", False, 2), (25, 40, 33, "f32", False, 2),
+    (25, 60, 40, "u8", True, 2), (25, 60, 36, "u8", False, 1), (25, 60, 36, "f32", False, 0)])
+def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt, given, show):
     """The env-step (sample, step, auto-reset, legal, observation) agrees with
     the oracle stepped with the same Philox choices: state, sorted CSR rows,
     canonical mask words and observations after every step. A 25-move cap
     makes games end and restart from the pool every 25 plies. Odd batch
-    sizes and both the u8 and the f32 observation. `given`: the caller passes
-    the actions instead, legal ones mixed with -1 and arbitrary (mostly
-    illegal) world ids, which leave their env as it was."""
-    print(f"[env_step] max_moves={max_moves} plies={plies} n={n} fmt={fmt} given={given}", flush=True)
+    sizes, the u8 and the f32 observation, HALF_DARK, DARK and BRIGHT.
+    `given`: the caller passes the actions instead, legal ones mixed with -1
+    and arbitrary (mostly illegal) world ids, which leave their env as it was."""
+    print(f"[env_step] max_moves={max_moves} plies={plies} n={n} fmt={fmt} given={given} show={show}", flush=True)
     rng = np.random.default_rng(n)
-    b = jq.JunqiBatch(n, show_mode=2, pool_size=128, max_num_moves=max_moves)
+    b = jq.JunqiBatch(n, show_mode=show, pool_size=128, max_num_moves=max_moves)
     b.reset(21)
-    games = G.oracle_games_from_lineups(jq.generate_lineups(21, n), 2, max_moves)
+    games = G.oracle_games_from_lineups(jq.generate_lineups(21, n), show, max_moves)
     b.legal()
     u8 = fmt == "u8"
     sp = torch.empty((n, 317, 17, 17), dtype=torch.uint8 if u8 else torch.float32, device=b.device)
@@ -497,7 +498,7 @@ def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt, given):
             assert bool(tm[i]) == bool(g.terminated), (ply, i)
             if g.terminated:
                 resets += 1
-                games[i] = O.Game(b.pool[G.reset_pool_index(i, ply, b.pool.shape[0])], show_mode=2,
+                games[i] = O.Game(b.pool[G.reset_pool_index(i, ply, b.pool.shape[0])], show_mode=show,
                                   max_num_moves=max_moves)
         G.compare_state(G.device_fields(b), G.oracle_fields(games), ctx=f"fused ply {ply}")
         offs = b.offsets.cpu().numpy(); vals = b.values.cpu().numpy(); mw = b.mask_words.cpu().numpy()
