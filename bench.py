@@ -33,6 +33,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--envs", type=int, default=32768)
     ap.add_argument("--fmt", default="u8", choices=["u8", "bf16", "f32"])
+    ap.add_argument("--path", default="fused", choices=["fused", "separate"],
+                    help="fused: jq_env_step; separate: the same step through jq_sample_uniform, jq_step, "
+                         "jq_reset_terminated and jq_legal, the reference collector's call order")
     ap.add_argument("--seed", type=int, default=0x4A51)
     ap.add_argument("--cpu-envs", type=int, default=4096)
     ap.add_argument("--cpu-steps", type=int, default=40)
@@ -152,9 +155,18 @@ def main() -> int:
         # Philox pick from the previous CSR rows, ply, restart from the pool,
         # next seat's sorted CSR + packed canonical mask (jq_env_step without
         # the observation, which is launched on its own so events can time it)
-        L.check(lib.jq_env_step(h, None, args.seed, ply, ply, b.counts.data_ptr(), b.offsets.data_ptr(),
-                                b.values.data_ptr(), b.mask_words.data_ptr(), fmt_code, None, None, None,
-                                term.data_ptr(), reward.data_ptr(), acts.data_ptr(), s))
+        if args.path == "fused":
+            L.check(lib.jq_env_step(h, None, args.seed, ply, ply, b.counts.data_ptr(), b.offsets.data_ptr(),
+                                    b.values.data_ptr(), b.mask_words.data_ptr(), fmt_code, None, None, None,
+                                    term.data_ptr(), reward.data_ptr(), acts.data_ptr(), s))
+        else:
+            L.check(lib.jq_sample_uniform(h, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
+                                          args.seed, ply, acts.data_ptr(), s))
+            L.check(lib.jq_step(h, acts.data_ptr(), None, L.ACT_WORLD, None, None, term.data_ptr(), None, None,
+                                None, None, reward.data_ptr(), None, s))
+            L.check(lib.jq_reset_terminated(h, ply, s))
+            L.check(lib.jq_legal(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
+                                 b.mask_words.data_ptr(), None, s))
         if ev_obs is not None:
             ev_obs[0].record()
         L.check(lib.jq_observe(h, None, fmt_code, 0, spatial.data_ptr(), P(aux), glob.data_ptr(), s))
@@ -198,6 +210,7 @@ def main() -> int:
         "data": "synthetic: seeded random legal setups, Philox-uniform legal actions, auto-reset from a 10000-setup pool",
         "config": {"workload": f"step + sorted legal CSR + packed canonical mask + 317-plane {args.fmt} obs "
                                f"of the acting seat, {n} games, HALF_DARK", "games": n, "obs_format": args.fmt,
+                   "path": args.path,
                    "mean_legal_actions": round(kbar, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
