@@ -808,7 +808,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     }
 }
 
-__global__ __launch_bounds__(64) void k_step(State S, const int32_t *__restrict__ actions,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_step(State S, const int32_t *__restrict__ actions,
                                              const int8_t *__restrict__ acting, int act_fmt, StepOut O)
 {
     const int env = blockIdx.x, l = threadIdx.x;
