@@ -1167,11 +1167,12 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
 }
 
 // Exclusive scan of counts into offsets (N+1); one 1024-thread block walks the
-// array in tiles of 32768 (one tile at the usual batch sizes): each thread
-// loads 32 consecutive counts with 16-byte loads, scans them in registers, the
-// 1024 thread totals are scanned by wave shuffles and the 16 wave totals
+// array in tiles of 32768 (one tile at the usual batch sizes). Wave w scans the
+// tile's 2048 counts from 2048 w on: lane l holds the four counts at 4 (64 k + l)
+// for k < 8, so every 16-byte load and store of the wave covers one contiguous
+// 1 KB; eight wave scans give the running sums, the 16 wave totals are scanned
 // through LDS, and a carry runs between tiles.
-constexpr int SCAN_THREADS = 1024, SCAN_ITEMS = 32, SCAN_TILE = SCAN_THREADS * SCAN_ITEMS;
+constexpr int SCAN_THREADS = 1024, SCAN_CHUNKS = 8, SCAN_TILE = SCAN_THREADS * 4 * SCAN_CHUNKS;
 __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                       int n)
 {
@@ -1181,24 +1182,31 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict
     const bool vec = ((reinterpret_cast<uintptr_t>(counts) | reinterpret_cast<uintptr_t>(offsets)) & 15) == 0;
     int carry = 0;
     for (int base = 0; base < n; base += SCAN_TILE) {
-        const int i0 = base + SCAN_ITEMS * t;
-        int v[SCAN_ITEMS];
-        if (vec && i0 + SCAN_ITEMS <= n) {
+        const int seg = base + w * 64 * 4 * SCAN_CHUNKS;
+        int4 v[SCAN_CHUNKS];
+        int excl[SCAN_CHUNKS];
+        int segsum = 0;
 #pragma unroll
-            for (int k = 0; k < SCAN_ITEMS / 4; ++k) {
-                const int4 c = reinterpret_cast<const int4 *>(counts + i0)[k];
-                v[4 * k] = c.x; v[4 * k + 1] = c.y; v[4 * k + 2] = c.z; v[4 * k + 3] = c.w;
+        for (int k = 0; k < SCAN_CHUNKS; ++k) {
+            const int i = seg + 4 * (64 * k + lane);
+            if (vec && i + 4 <= n) {
+                v[k] = *reinterpret_cast<const int4 *>(counts + i);
+            } else {
+                v[k].x = i < n ? counts[i] : 0;
+                v[k].y = i + 1 < n ? counts[i + 1] : 0;
+                v[k].z = i + 2 < n ? counts[i + 2] : 0;
+                v[k].w = i + 3 < n ? counts[i + 3] : 0;
             }
-        } else {
-#pragma unroll
-            for (int k = 0; k < SCAN_ITEMS; ++k) v[k] = i0 + k < n ? counts[i0 + k] : 0;
         }
-        int tsum = 0;
 #pragma unroll
-        for (int k = 0; k < SCAN_ITEMS; ++k) tsum += v[k];
-        int incl = tsum;
-        for (int o = 1; o < 64; o <<= 1) { const int u = __shfl_up(incl, o); if (lane >= o) incl += u; }
-        if (lane == 63) wsum[w] = incl;
+        for (int k = 0; k < SCAN_CHUNKS; ++k) {
+            const int s4 = v[k].x + v[k].y + v[k].z + v[k].w;
+            int incl = s4;
+            for (int o = 1; o < 64; o <<= 1) { const int u = __shfl_up(incl, o); if (lane >= o) incl += u; }
+            excl[k] = segsum + incl - s4;
+            segsum += __shfl(incl, 63);
+        }
+        if (lane == 0) wsum[w] = segsum;
         __syncthreads();
         if (w == 0) {
             const int x = lane < SCAN_THREADS / 64 ? wsum[lane] : 0;
@@ -1208,22 +1216,22 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict
             if (lane == SCAN_THREADS / 64 - 1) tile_total = y;
         }
         __syncthreads();
-        int run = carry + wsum[w] + incl - tsum;
-        if (vec && i0 + SCAN_ITEMS <= n) {
+        const int wbase = carry + wsum[w];
 #pragma unroll
-            for (int k = 0; k < SCAN_ITEMS / 4; ++k) {
-                int4 o;
-                o.x = run; run += v[4 * k];
-                o.y = run; run += v[4 * k + 1];
-                o.z = run; run += v[4 * k + 2];
-                o.w = run; run += v[4 * k + 3];
-                reinterpret_cast<int4 *>(offsets + i0)[k] = o;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < SCAN_ITEMS; ++k) {
-                if (i0 + k < n) offsets[i0 + k] = run;
-                run += v[k];
+        for (int k = 0; k < SCAN_CHUNKS; ++k) {
+            const int i = seg + 4 * (64 * k + lane);
+            int4 o;
+            o.x = wbase + excl[k];
+            o.y = o.x + v[k].x;
+            o.z = o.y + v[k].y;
+            o.w = o.z + v[k].z;
+            if (vec && i + 4 <= n) {
+                *reinterpret_cast<int4 *>(offsets + i) = o;
+            } else {
+                if (i < n) offsets[i] = o.x;
+                if (i + 1 < n) offsets[i + 1] = o.y;
+                if (i + 2 < n) offsets[i + 2] = o.z;
+                if (i + 3 < n) offsets[i + 3] = o.w;
             }
         }
         carry += tile_total;
