@@ -182,6 +182,43 @@ void jqo_tables_export(int8_t *on_board, int8_t *is_rail, int8_t *is_camp, int8_
 }
 
 /* ======================================================================
+ * Rotation into an acting seat's canonical frame (junqi_core/rotation.py:44-80)
+ * and seat-local placement (board.py:88-102)
+ * ====================================================================== */
+void jqo_world_to_canonical(int x, int y, int seat, int *cx, int *cy)
+{
+    switch (seat & 3) {
+    case 0: *cx = x; *cy = y; break;                 /* SOUTH: identity */
+    case 1: *cx = y; *cy = 16 - x; break;            /* WEST: +90 deg */
+    case 2: *cx = 16 - x; *cy = 16 - y; break;       /* NORTH: 180 deg */
+    default: *cx = 16 - y; *cy = x; break;           /* EAST: -90 deg */
+    }
+}
+
+void jqo_canonical_to_world(int cx, int cy, int seat, int *x, int *y)
+{
+    switch (seat & 3) {
+    case 0: *x = cx; *y = cy; break;
+    case 1: *x = 16 - cy; *y = cx; break;
+    case 2: *x = 16 - cx; *y = 16 - cy; break;
+    default: *x = cy; *y = 16 - cx; break;
+    }
+}
+
+void jqo_index_to_pos(int seat, int i, int *x, int *y) { seat_pos(seat & 3, i, x, y); }
+
+int jqo_canonical_id(int seat, int world_id)
+{   /* compact canonical action id of `seat` (junqi_rl/action_lut.py:62-170) */
+    int src = world_id / NC, dst = world_id % NC, a[2] = {src, dst}, c[2];
+    for (int q = 0; q < 2; q++) {
+        int cx, cy;
+        jqo_world_to_canonical(a[q] % 17, a[q] / 17, seat, &cx, &cy);
+        c[q] = T_f2c[cy * 17 + cx];
+    }
+    return c[0] * JQO_ONB + c[1];
+}
+
+/* ======================================================================
  * CPython random.Random (stdlib): MT19937 init_by_array, getrandbits,
  * _randbelow_with_getrandbits, shuffle, choice.
  * ====================================================================== */
@@ -295,6 +332,29 @@ void jqo_setup_pool(uint64_t seed, int32_t pool_size, int8_t *pool)
     jqo_mt r; jqo_mt_seed(&r, seed);
     for (int p = 0; p < pool_size; p++)
         for (int s = 0; s < 4; s++) jqo_random_lineup(&r, pool + (size_t)p * 120 + 30 * s);
+}
+
+/* validate_lineup (junqi_core/setup.py:60-136): violation bits of one seat's
+ * 30-entry lineup, 0 when it satisfies C1-C5. A value that is not a PieceType
+ * (0..13) is a TYPE violation and stops the check, as PieceType(int(p)) raising
+ * does there. */
+int jqo_validate_lineup(const int8_t lu[30])
+{
+    int v = 0, cnt[14] = {0}, nflag = 0, flag_i = -1;
+    for (int i = 0; i < 30; i++) if (lu[i] < 0 || lu[i] > JQO_GONGB) return JQO_V_TYPE;
+    for (int i = 0; i < 30; i++) {
+        int t = lu[i];
+        cnt[t]++;
+        if (is_camp_idx(i) && t != JQO_NONE) v |= JQO_V_C1;
+        if (t == JQO_JUNQI) { nflag++; flag_i = i; }
+        if (t == JQO_DILEI && i < 20) v |= JQO_V_C3;        /* BACK_TWO_ROWS = 20..29 */
+        if (t == JQO_ZHADAN && i < 5) v |= JQO_V_C4;        /* FRONT_ROW = 0..4 */
+    }
+    if (nflag != 1 || !is_sh_idx(flag_i)) v |= JQO_V_C2;
+    if (cnt[JQO_NONE] != 5) v |= JQO_V_C5;
+    for (int t = JQO_JUNQI; t <= JQO_GONGB; t++) if (cnt[t] != PIECE_COUNTS[t]) v |= JQO_V_C5;
+    if (cnt[JQO_DARK] != 0) v |= JQO_V_C5;
+    return v;
 }
 
 /* ======================================================================
@@ -864,6 +924,20 @@ static void cm_apply(jqo_game *g, int is_eat, int apid, int dpid, int aseat, int
     }
 }
 
+/* apply_combat_event (combat_memory.py:354-569) and apply_path_revealed_gongb
+ * (combat_memory.py:339-351) on a game's combat memory, for hand-built cases.
+ * The defender's cell argument of the reference is not read by the update. */
+void jqo_cm_apply_event(jqo_game *g, int is_eat, int apid, int dpid, int aseat, int dseat, int atype, int dtype,
+                        int step)
+{
+    cm_apply(g, is_eat, apid, dpid, aseat, dseat, atype, dtype, step);
+}
+
+void jqo_cm_path_revealed_gongb(jqo_game *g, int pid)
+{
+    for (int o = 0; o < 4; o++) g->cm_is_gongb[o][pid] = 1;
+}
+
 /* ======================================================================
  * GameState construction (state.py:490-620, 346-483)
  * ====================================================================== */
@@ -1252,13 +1326,8 @@ static void observe_impl(const jqo_game *g, int obs, const float *ext, float *ou
     /* rotate into the canonical frame (rotation.py:44-64, 112-149) */
     for (int c = 0; c < JQO_OBS_C; c++)
         for (int f = 0; f < NC; f++) {
-            int x = f % 17, y = f / 17, cx, cy;
-            switch (obs) {
-            case 0: cx = x; cy = y; break;
-            case 1: cx = y; cy = 16 - x; break;
-            case 2: cx = 16 - x; cy = 16 - y; break;
-            default: cx = 16 - y; cy = x; break;
-            }
+            int cx, cy;
+            jqo_world_to_canonical(f % 17, f / 17, obs, &cx, &cy);
             out[(size_t)c * NC + cy * 17 + cx] = W(c, f);
         }
 #undef W
@@ -1301,15 +1370,7 @@ long jqo_batch_env_step(jqo_game *gs, int n, const int32_t *actions, int32_t *le
         memset(bits, 0, 2081);
         int s = g->turn;
         for (int j = 0; j < k; j++) {   /* canonical compact bitmask */
-            int src = ids[j] / NC, dst = ids[j] % NC;
-            int a[2] = {src, dst}, c[2];
-            for (int q = 0; q < 2; q++) {
-                int x = a[q] % 17, y = a[q] / 17, cx, cy;
-                switch (s) { case 0: cx = x; cy = y; break; case 1: cx = y; cy = 16 - x; break;
-                             case 2: cx = 16 - x; cy = 16 - y; break; default: cx = 16 - y; cy = x; }
-                c[q] = T_f2c[cy * 17 + cx];
-            }
-            int bit = c[0] * JQO_ONB + c[1];
+            int bit = jqo_canonical_id(s, ids[j]);
             bits[bit >> 3] |= (uint8_t)(1u << (bit & 7));
         }
         legal_counts[i] = k;
@@ -1318,4 +1379,108 @@ long jqo_batch_env_step(jqo_game *gs, int n, const int32_t *actions, int32_t *le
             jqo_observe(g, g->turn, obs_spatial + (size_t)i * JQO_OBS_C * NC, obs_global + (size_t)i * JQO_OBS_G);
     }
     return total;
+}
+
+/* ======================================================================
+ * Samplers (config c2 / c5 action streams; the reference draws its random
+ * opponent as the argmax of Gumbel noise over the legal canonical ids,
+ * junqi_rl/training/gpu_collector.py:799-810). Philox4x32-10 is the published
+ * counter-based generator (Salmon, Moraes, Dror, Shaw, SC'11), restated here
+ * and pinned by the Random123 known-answer vectors.
+ * ====================================================================== */
+void jqo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])
+{
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; r++) {
+        uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1; c3 = (uint32_t)p0; c0 = n0; c2 = n2;
+        k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+static uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint64_t seed)
+{
+    uint32_t ctr[4] = {c0, c1, c2, c3}, key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)}, out[4];
+    jqo_philox4x32_10(ctr, key, out);
+    return out[0];
+}
+
+/* Uniform pick from a legal row: index = (u * n) >> 32 with u = word 0 of
+ * Philox(counter (env, ply lo, ply hi, 0), key seed); -1 for an empty row. */
+int32_t jqo_sample_uniform(const int32_t *ids, int n, int env, uint64_t seed, uint64_t ply)
+{
+    if (n <= 0) return -1;
+    uint32_t u = philox_w0((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u, seed);
+    return ids[(int)(((uint64_t)u * (uint64_t)n) >> 32)];
+}
+
+/* Masked-logit pick: every canonical action id c of the acting seat carries an
+ * i.i.d. N(0,1) logit z_c = Phi^-1((u_c + 1/2) / 2^32), u_c = word 0 of
+ * Philox(counter (env, ply lo, ply hi, 1 + c), key seed); the action is the
+ * argmax of z over the legal set. Phi^-1 is strictly increasing, so that is the
+ * argmax of u_c itself (ties to the lowest canonical id, as torch.argmax takes
+ * the first maximum). Returns the world id (-1 for an empty row) and the
+ * canonical id through *canon. */
+int32_t jqo_sample_logits(const int32_t *ids, int n, int seat, int env, uint64_t seed, uint64_t ply, int32_t *canon)
+{
+    int32_t best = -1, bc = -1;
+    uint32_t bu = 0;
+    for (int j = 0; j < n; j++) {
+        int c = jqo_canonical_id(seat, ids[j]);
+        uint32_t u = philox_w0((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), (uint32_t)(1 + c), seed);
+        if (best < 0 || u > bu || (u == bu && c < bc)) { best = ids[j]; bc = c; bu = u; }
+    }
+    if (canon) *canon = bc;
+    return best;
+}
+
+/* Pool entry a finished env restarts from (src/env/cuda/src/game_state.cu:2997-3001). */
+int32_t jqo_reset_pool_index(int env, int64_t seed, int pool_size)
+{
+    uint64_t h = (uint64_t)env * 2654435761ull + (uint64_t)seed;
+    h ^= h >> 17;
+    h *= 0xbf58476d1ce4e5b9ull;
+    h ^= h >> 31;
+    return (int32_t)(h % (uint64_t)pool_size);
+}
+
+/* `steps` rollout env-steps of n games (OpenMP over games): at env-step k each
+ * game draws its action from the acting seat's legal ids with `sampler` (0
+ * uniform, 1 masked logits) under (seed, ply0 + k), applies it, records the
+ * acting team's reward (+-1 on the ply that ends the game), the terminated
+ * flag and the Zobrist hash after the ply, then a finished game restarts from
+ * pool[jqo_reset_pool_index(i, reset_seed0 + k)]. Outputs are (steps, n)
+ * row-major; any may be NULL. Returns the number of plies applied. */
+long jqo_batch_rollout(jqo_game *gs, int n, const int8_t *pool, int pool_size, int sampler, uint64_t seed,
+                       uint64_t ply0, int64_t reset_seed0, int steps, float *reward, uint8_t *done,
+                       uint64_t *hash, int32_t *actions)
+{
+    long applied = 0;
+#pragma omp parallel for schedule(dynamic, 16) reduction(+:applied)
+    for (int i = 0; i < n; i++) {
+        jqo_game *g = &gs[i];
+        int32_t ids[4096];
+        for (int k = 0; k < steps; k++) {
+            size_t o = (size_t)k * n + i;
+            int seat = g->turn, m = jqo_legal_ids(g, seat, ids, 4096);
+            int32_t a = sampler ? jqo_sample_logits(ids, m, seat, i, seed, ply0 + k, NULL)
+                                : jqo_sample_uniform(ids, m, i, seed, ply0 + k);
+            jqo_result r;
+            memset(&r, 0, sizeof r);
+            int rc = a >= 0 ? jqo_step(g, a / NC, a % NC, &r) : -1;
+            if (rc == 0) applied++;
+            if (actions) actions[o] = a;
+            if (reward) reward[o] = (rc == 0 && r.terminated && !r.draw && r.winner >= 0)
+                                        ? ((seat & 1) == r.winner ? 1.f : -1.f) : 0.f;
+            if (done) done[o] = (uint8_t)(g->terminated != 0);
+            if (hash) hash[o] = g->zobrist;
+            if (g->terminated && pool && pool_size > 0) {
+                int p = jqo_reset_pool_index(i, reset_seed0 + k, pool_size);
+                jqo_new_game(g, pool + (size_t)p * 120, g->show_mode, g->max_num_moves);
+            }
+        }
+    }
+    return applied;
 }

@@ -126,6 +126,34 @@ void jqo_observe_ext(const jqo_game *g, int observer, const float *ext /*12*289*
 uint64_t jqo_recompute_zobrist(const jqo_game *g);
 void jqo_belief_row(int code, float out[12]);
 
+/* ---- rotation (rotation.py:44-80), placement (board.py:88-102), action codec ---- */
+void jqo_world_to_canonical(int x, int y, int seat, int *cx, int *cy);
+void jqo_canonical_to_world(int cx, int cy, int seat, int *x, int *y);
+void jqo_index_to_pos(int seat, int i, int *x, int *y);
+/* compact canonical id FLAT_TO_COMPACT[rot(src)]*129 + FLAT_TO_COMPACT[rot(dst)] of a world id */
+int  jqo_canonical_id(int seat, int world_id);
+
+/* ---- setup validation (setup.py:60-136) ---- */
+#define JQO_V_TYPE 1   /* a value that is not a PieceType */
+#define JQO_V_C1 2     /* camp not empty */
+#define JQO_V_C2 4     /* not exactly one flag, or flag outside a stronghold */
+#define JQO_V_C3 8     /* landmine outside the back two rows */
+#define JQO_V_C4 16    /* bomb in the front row */
+#define JQO_V_C5 32    /* piece counts */
+int  jqo_validate_lineup(const int8_t lineup[30]);
+
+/* ---- CombatMemory on hand-built cases (combat_memory.py:339-569) ---- */
+void jqo_cm_apply_event(jqo_game *g, int is_eat, int apid, int dpid, int aseat, int dseat, int atype, int dtype,
+                        int step);
+void jqo_cm_path_revealed_gongb(jqo_game *g, int pid);
+
+/* ---- samplers (Philox4x32-10, Salmon et al. SC'11) ---- */
+void    jqo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+int32_t jqo_sample_uniform(const int32_t *ids, int n, int env, uint64_t seed, uint64_t ply);
+int32_t jqo_sample_logits(const int32_t *ids, int n, int seat, int env, uint64_t seed, uint64_t ply,
+                          int32_t *canon);
+int32_t jqo_reset_pool_index(int env, int64_t seed, int pool_size);
+
 /* ---- batch (CPU baseline; OpenMP over envs) ---- */
 int  jqo_sizeof_game(void);
 int  jqo_omp_threads(void);
@@ -135,6 +163,13 @@ void jqo_batch_new(jqo_game *gs, int n, const int8_t *setups, int show_mode, int
  * Returns total legal-id count. */
 long jqo_batch_env_step(jqo_game *gs, int n, const int32_t *actions, int32_t *legal_counts,
                         uint8_t *mask_bits, float *obs_spatial, float *obs_global, int write_obs);
+
+/* Rollout: `steps` env-steps of sample (0 uniform, 1 masked logits) -> step ->
+ * record reward / done / hash -> restart finished games from the pool.
+ * Outputs (steps, n) row-major, any may be NULL. */
+long jqo_batch_rollout(jqo_game *gs, int n, const int8_t *pool, int pool_size, int sampler, uint64_t seed,
+                       uint64_t ply0, int64_t reset_seed0, int steps, float *reward, uint8_t *done,
+                       uint64_t *hash, int32_t *actions);
 
 #ifdef __cplusplus
 }

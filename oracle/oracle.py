@@ -103,6 +103,21 @@ def lib() -> C.CDLL:
     L.jqo_batch_env_step.argtypes = [P, C.c_int, P, P, P, P, P, C.c_int]
     L.jqo_batch_env_step.restype = C.c_long
     L.jqo_tables_export.argtypes = [P] * 9
+    I = C.c_int
+    L.jqo_world_to_canonical.argtypes = [I, I, I, P, P]
+    L.jqo_canonical_to_world.argtypes = [I, I, I, P, P]
+    L.jqo_index_to_pos.argtypes = [I, I, P, P]
+    L.jqo_canonical_id.argtypes = [I, I]; L.jqo_canonical_id.restype = I
+    L.jqo_validate_lineup.argtypes = [P]; L.jqo_validate_lineup.restype = I
+    L.jqo_cm_apply_event.argtypes = [P, I, I, I, I, I, I, I, I]
+    L.jqo_cm_path_revealed_gongb.argtypes = [P, I]
+    L.jqo_philox4x32_10.argtypes = [P, P, P]
+    L.jqo_sample_uniform.argtypes = [P, I, I, C.c_uint64, C.c_uint64]; L.jqo_sample_uniform.restype = C.c_int32
+    L.jqo_sample_logits.argtypes = [P, I, I, I, C.c_uint64, C.c_uint64, P]
+    L.jqo_sample_logits.restype = C.c_int32
+    L.jqo_reset_pool_index.argtypes = [I, C.c_int64, I]; L.jqo_reset_pool_index.restype = C.c_int32
+    L.jqo_batch_rollout.argtypes = [P, I, P, I, I, C.c_uint64, C.c_uint64, C.c_int64, I, P, P, P, P]
+    L.jqo_batch_rollout.restype = C.c_long
     L.jqo_init()
     assert L.jqo_sizeof_game() == GAME_DTYPE.itemsize, (L.jqo_sizeof_game(), GAME_DTYPE.itemsize)
     if RECENCY_LUT_PATH.exists():
@@ -256,12 +271,87 @@ class Game:
             lib().jqo_observe_ext(_p(self.buf), observer, _p(b), _p(sp), _p(gl))
         return sp, gl
 
+    def cm_apply_event(self, *, is_eat: bool, attacker_pid: int, defender_pid: int, attacker_seat: int,
+                       defender_seat: int, attacker_type: int, defender_type: int, step: int) -> None:
+        """apply_combat_event (combat_memory.py:354-569) on this game's memory."""
+        lib().jqo_cm_apply_event(_p(self.buf), int(is_eat), attacker_pid, defender_pid, attacker_seat,
+                                 defender_seat, attacker_type, defender_type, step)
+
+    def cm_path_revealed_gongb(self, pid: int) -> None:
+        lib().jqo_cm_path_revealed_gongb(_p(self.buf), pid)
+
     def recompute_zobrist(self) -> int:
         return int(lib().jqo_recompute_zobrist(_p(self.buf)))
 
     @property
     def zobrist_i64(self) -> int:
         return int(np.int64(self.buf[0]["zobrist"].view(np.int64)))
+
+
+def world_to_canonical(x: int, y: int, seat: int) -> tuple[int, int]:
+    """rotation.world_to_canonical (rotation.py:44-61)."""
+    cx, cy = C.c_int(), C.c_int()
+    lib().jqo_world_to_canonical(x, y, seat, C.byref(cx), C.byref(cy))
+    return cx.value, cy.value
+
+
+def canonical_to_world(x: int, y: int, seat: int) -> tuple[int, int]:
+    """rotation.canonical_to_world (rotation.py:64-80)."""
+    wx, wy = C.c_int(), C.c_int()
+    lib().jqo_canonical_to_world(x, y, seat, C.byref(wx), C.byref(wy))
+    return wx.value, wy.value
+
+
+def index_to_pos(seat: int, i: int) -> tuple[int, int]:
+    """board.index_to_pos (board.py:88-102)."""
+    x, y = C.c_int(), C.c_int()
+    lib().jqo_index_to_pos(seat, i, C.byref(x), C.byref(y))
+    return x.value, y.value
+
+
+def canonical_id(seat: int, world_id: int) -> int:
+    return int(lib().jqo_canonical_id(seat, world_id))
+
+
+# violation bits of validate_lineup (setup.py:60-136)
+V_TYPE, V_C1, V_C2, V_C3, V_C4, V_C5 = 1, 2, 4, 8, 16, 32
+V_NAMES = {V_TYPE: "TYPE", V_C1: "C1", V_C2: "C2", V_C3: "C3", V_C4: "C4", V_C5: "C5"}
+
+
+def validate_lineup(lineup) -> set[str]:
+    """Violation codes of one seat's 30-entry lineup (empty set = valid)."""
+    lu = np.ascontiguousarray(np.asarray(lineup, dtype=np.int64))
+    if lu.size != 30:
+        return {"LENGTH"}
+    if (lu < -128).any() or (lu > 127).any():
+        return {"TYPE"}
+    v = int(lib().jqo_validate_lineup(_p(np.ascontiguousarray(lu.astype(np.int8)))))
+    return {name for bit, name in V_NAMES.items() if v & bit}
+
+
+def philox4x32_10(ctr, key) -> tuple[int, int, int, int]:
+    c = np.asarray(ctr, dtype=np.uint32)
+    k = np.asarray(key, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    lib().jqo_philox4x32_10(_p(c), _p(k), _p(out))
+    return tuple(int(v) for v in out)
+
+
+def sample_uniform(ids: np.ndarray, env: int, seed: int, ply: int) -> int:
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    return int(lib().jqo_sample_uniform(_p(ids), len(ids), env, seed, ply))
+
+
+def sample_logits(ids: np.ndarray, seat: int, env: int, seed: int, ply: int) -> tuple[int, int]:
+    """(world id, canonical id) of the masked N(0,1)-logit argmax."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    c = C.c_int32(-1)
+    w = int(lib().jqo_sample_logits(_p(ids), len(ids), seat, env, seed, ply, C.byref(c)))
+    return w, int(c.value)
+
+
+def reset_pool_index(env: int, seed: int, pool_size: int) -> int:
+    return int(lib().jqo_reset_pool_index(env, seed, pool_size))
 
 
 def belief_row(code: int) -> np.ndarray:
@@ -299,6 +389,20 @@ class Batch:
             raise ValueError("obs=True needs obs_spatial and obs_global buffers")
         return int(lib().jqo_batch_env_step(_p(self.games), self.n, _p(actions), _p(self.counts),
                                             mb, sp, gl, 1 if obs else 0))
+
+
+def rollout(batch: "Batch", pool: np.ndarray, *, sampler: int, seed: int, ply0: int, reset_seed0: int,
+            steps: int) -> dict:
+    """jqo_batch_rollout over a Batch: (steps, n) reward / done / hash / actions."""
+    n = batch.n
+    pool = np.ascontiguousarray(pool, dtype=np.int8).reshape(-1, 120)
+    out = {"reward": np.zeros((steps, n), np.float32), "done": np.zeros((steps, n), np.uint8),
+           "hash": np.zeros((steps, n), np.uint64), "actions": np.zeros((steps, n), np.int32)}
+    applied = lib().jqo_batch_rollout(_p(batch.games), n, _p(pool), len(pool), sampler, seed, ply0, reset_seed0,
+                                      steps, _p(out["reward"]), _p(out["done"]), _p(out["hash"]),
+                                      _p(out["actions"]))
+    out["applied"] = int(applied)
+    return out
 
 
 def omp_threads() -> int:
