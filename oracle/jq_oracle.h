@@ -10,9 +10,13 @@
  * junqi_core/state.py::GameState; where BatchedGameState diverges from it,
  * GameState's behaviour is the one restated.
  *
- * Parity unpinned (jqo_observe): DARK-mode teammate belief values after the
- * first ply beyond the probability-vector invariants the tests check, and
- * combat-memory / belief values beyond step 100 of the reference's hashed games.
+ * How it is pinned (tests/test_oracle*.py): the reference's golden scenarios,
+ * observation hashes and recorded game; its known-answer tests (rotation,
+ * combat memory, beliefs, setup validation) restated; the 4-fold rotation
+ * symmetry of the rules; and 12 complete reference games (Zobrist hash after
+ * every ply; combat memory, beliefs and all four observers' float32
+ * observations bit for bit at seven plies each, BRIGHT / DARK / HALF_DARK)
+ * written by tests/golden/gen_reference_vectors.py.
  */
 #ifndef JQ_ORACLE_H
 #define JQ_ORACLE_H
