@@ -156,17 +156,18 @@ def main() -> int:
         # next seat's sorted CSR + packed canonical mask (jq_env_step without
         # the observation, which is launched on its own so events can time it)
         if args.path == "fused":
-            L.check(lib.jq_env_step(h, None, args.seed, ply, ply, b.counts.data_ptr(), b.offsets.data_ptr(),
-                                    b.values.data_ptr(), b.mask_words.data_ptr(), fmt_code, None, None, None,
-                                    term.data_ptr(), reward.data_ptr(), acts.data_ptr(), s))
+            L.check(lib.jq_env_step(h, None, L.SAMPLE_UNIFORM, args.seed, ply, ply, b.counts.data_ptr(),
+                                    b.offsets.data_ptr(), b.values.data_ptr(), b.values.numel(),
+                                    b.mask_words.data_ptr(), fmt_code, None, None, None, term.data_ptr(),
+                                    reward.data_ptr(), None, acts.data_ptr(), s))
         else:
             L.check(lib.jq_sample_uniform(h, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
-                                          args.seed, ply, acts.data_ptr(), s))
+                                          b.values.numel(), args.seed, ply, acts.data_ptr(), s))
             L.check(lib.jq_step(h, acts.data_ptr(), None, L.ACT_WORLD, None, None, term.data_ptr(), None, None,
                                 None, None, reward.data_ptr(), None, s))
             L.check(lib.jq_reset_terminated(h, ply, s))
             L.check(lib.jq_legal(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
-                                 b.mask_words.data_ptr(), None, s))
+                                 b.values.numel(), b.mask_words.data_ptr(), None, s))
         if ev_obs is not None:
             ev_obs[0].record()
         L.check(lib.jq_observe(h, None, fmt_code, 0, spatial.data_ptr(), P(aux), glob.data_ptr(), s))

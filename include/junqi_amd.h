@@ -39,6 +39,19 @@ extern "C" {
 #define JQ_E_STATE (-2)    /* handle not ready (tables / pool missing) */
 #define JQ_E_HIP (-3)      /* HIP runtime error */
 #define JQ_E_OOM (-4)      /* device allocation failed */
+#define JQ_E_CAPACITY (-5) /* an output buffer is smaller than the result */
+
+/* lineup violation bits of jq_validate_lineup (setup.py:60-136) */
+#define JQ_LINEUP_TYPE 1   /* a value that is not a PieceType (0..13) */
+#define JQ_LINEUP_C1 2     /* a camp slot holds a piece */
+#define JQ_LINEUP_C2 4     /* not exactly one flag, or the flag outside the strongholds */
+#define JQ_LINEUP_C3 8     /* a landmine outside the back two rows */
+#define JQ_LINEUP_C4 16    /* a bomb in the front row */
+#define JQ_LINEUP_C5 32    /* piece counts differ from PIECE_COUNTS */
+
+/* samplers of jq_env_step */
+#define JQ_SAMPLE_UNIFORM 0 /* Philox pick uniform over the legal CSR row */
+#define JQ_SAMPLE_LOGITS 1  /* argmax of i.i.d. N(0,1) logits over the legal canonical ids */
 
 /* observation output formats */
 #define JQ_OBS_F32 0       /* (N,317,17,17) float32, the reference layout */
@@ -70,13 +83,27 @@ int jq_upload_zobrist(jq_env *env, const uint64_t *host_table, int64_t count);
 /* Recency table float32[4][4096] (observation.py:1552-1567 values). Host pointer. */
 int jq_upload_recency(jq_env *env, const float *host_lut);
 
-/* Setup pool (pool_size,120) int8 piece types per pid, host pointer. Replaces
+/* validate_lineup (junqi_core/setup.py:60-136) of one seat's 30 slot types:
+ * returns 0 when C1-C5 hold, else the JQ_LINEUP_* bits of every rule broken
+ * (JQ_LINEUP_TYPE alone when a value is not a PieceType), or JQ_E_ARG for a
+ * null pointer. Host only. */
+int jq_validate_lineup(const int8_t *lineup30);
+
+/* Setup pool (pool_size,120) int8 piece types per pid, host pointer. Every
+ * seat's lineup must pass jq_validate_lineup, else JQ_E_ARG names the first
+ * bad entry and the handle keeps its previous pool. The pool buffer is
+ * reused while the new pool fits and replaced (after a device sync) when it
+ * grows, so repeated uploads hold one buffer. Replaces
  * junqi_cuda.upload_setup_pool (junqi_rl/gpu_rollout.py:588-652). */
 int jq_upload_setup_pool(jq_env *env, const int8_t *host_pool, int32_t pool_size);
 
 /* Start every env from the given lineups ((N,120) int8 piece types per pid, host
  * pointer): GameState.new_game + BeliefTensor.initial for all four observers.
- * Replaces GpuRollout.reset's copy_from_host path (junqi_rl/gpu_rollout.py:690-744). */
+ * Lineups are validated as GameState.new_game does (state.py:498-507): a
+ * violation returns JQ_E_ARG naming the env and seat, and no env is touched.
+ * Replaces GpuRollout.reset's copy_from_host path (junqi_rl/gpu_rollout.py:690-744).
+ * A CSR from before the reset no longer describes the games: call jq_legal
+ * before sampling from one (jq_env_step's sampler reads the CSR it is given). */
 int jq_reset_lineups(jq_env *env, const int8_t *host_lineups, void *stream);
 
 /* Host-side lineup generation identical to junqi_core.setup.generate_random_setup
@@ -106,7 +133,7 @@ int jq_board_tables(void *host_out, int64_t nbytes);
 
 /* Reset terminated envs from the pool, picking entry hash(env, seed) % pool_size
  * (src/env/cuda/src/game_state.cu:2936-3102). Replaces reset_terminated_envs
- * (gpu_rollout.py:1007-1028). `mask` (device uint8, N) optionally limits it. */
+ * (gpu_rollout.py:1007-1028). */
 int jq_reset_terminated(jq_env *env, int64_t seed, void *stream);
 
 /* Apply one ply per env. actions: device int32 (N) in `action_format`; acting:
@@ -123,14 +150,18 @@ int jq_step(jq_env *env, const int32_t *actions, const int8_t *acting, int32_t a
 
 /* Legal actions of `acting` (device int8 N; NULL = current turn) for every env.
  * counts: device int32 (N); offsets: device int32 (N+1), exclusive scan of counts;
- * values: device int32 (capacity >= N*JQ_MAX_LEGAL), per-env ascending world ids
+ * values: device int32 of values_capacity elements, per-env ascending world ids
  * src*289+dst (move_gen.py:1199 order); mask_words: device int32 (N, 521) packed
  * canonical compact mask; mask_bool: device uint8 (N, 16641) (gpu_rollout.py:1220).
- * Any output may be NULL (offsets/values need counts). Replaces
- * legal_action_ids_batch_csr (game_state.cu:1892-1962) and
- * legal_mask_canonical_batch (game_state.cu:2291-2508). */
+ * Any output may be NULL (offsets/values need counts). values_capacity >=
+ * N*JQ_MAX_LEGAL can never overflow and the call stays asynchronous; a smaller
+ * capacity makes the call read the total (offsets[N]) back, as the reference's
+ * CSR call does (game_state.cu:1936-1948), and return JQ_E_CAPACITY without
+ * writing values when the ids do not fit (counts and offsets are written). No
+ * kernel writes past values_capacity. Replaces legal_action_ids_batch_csr
+ * (game_state.cu:1892-1962) and legal_mask_canonical_batch (game_state.cu:2291-2508). */
 int jq_legal(jq_env *env, const int8_t *acting, int32_t *counts, int32_t *offsets, int32_t *values,
-             int32_t *mask_words, uint8_t *mask_bool, void *stream);
+             int64_t values_capacity, int32_t *mask_words, uint8_t *mask_bool, void *stream);
 
 /* Per-piece slot mask of `acting` (device int8 N; NULL = current turn):
  * slots: device uint8 (N, 120, 80), 16-byte aligned; slots[i][pid][s] = 1 iff
@@ -169,19 +200,39 @@ int jq_clear_beliefs(jq_env *env);
 /* The 256-entry float32 decode table of JQ_OBS_U8 codes (host pointer out). */
 int jq_obs_decode_table(float *host_out256);
 
-/* Sampler: world action per env drawn uniformly from its legal row with Philox4x32-10
- * keyed (seed, ply) and counter (env) -- index = (u32 * count) >> 32. Needs the
- * counts/offsets/values of jq_legal. Writes -1 for envs with no legal action. */
+/* Samplers over the CSR jq_legal / jq_env_step wrote for the current state
+ * (values_capacity as given there; a row that does not lie inside it, or an
+ * empty row, gives -1). Counter-based Philox4x32-10 (Salmon et al., SC'11),
+ * key (seed lo, seed hi):
+ * jq_sample_uniform: index = (u * count) >> 32, u = word 0 of counter
+ *   (env, ply lo, ply hi, 0); the world id values[offsets[env] + index].
+ * jq_sample_logits: every canonical id c of the acting seat (`acting`, device
+ *   int8 N; NULL = current turn) carries the logit z_c = Phi^-1((u_c + 1/2) / 2^32),
+ *   u_c = word 0 of counter (env, ply lo, ply hi, 1 + c), i.i.d. N(0,1); the
+ *   pick is the argmax of z over the legal ids (ties to the lowest c, as
+ *   torch.argmax), computed exactly as the argmax of u_c. The reference's
+ *   random opponent is this argmax with Gumbel noise over the legal mask
+ *   (junqi_rl/training/gpu_collector.py:799-810). actions_out gets the world id,
+ *   canonical_out (may be NULL) the canonical id. */
 int jq_sample_uniform(jq_env *env, const int32_t *counts, const int32_t *offsets, const int32_t *values,
-                      uint64_t seed, uint64_t ply, int32_t *actions_out, void *stream);
+                      int64_t values_capacity, uint64_t seed, uint64_t ply, int32_t *actions_out, void *stream);
+int jq_sample_logits(jq_env *env, const int8_t *acting, const int32_t *counts, const int32_t *offsets,
+                     const int32_t *values, int64_t values_capacity, uint64_t seed, uint64_t ply,
+                     int32_t *actions_out, int32_t *canonical_out, void *stream);
 
-/* One fused env-step for the whole batch: sample (if actions == NULL) -> step ->
- * auto-reset terminated envs from the pool -> legal (counts/offsets/values/mask) ->
- * observation of the new acting seat. Buffers as in the calls above. */
-int jq_env_step(jq_env *env, const int32_t *actions, uint64_t sample_seed, uint64_t ply,
-                int64_t reset_seed, int32_t *counts, int32_t *offsets, int32_t *values,
+/* One fused env-step for the whole batch: sample with `sampler` (JQ_SAMPLE_*,
+ * from the CSR of the previous call, if actions == NULL) -> step -> auto-reset
+ * terminated envs from the pool -> legal (counts/offsets/values/mask) ->
+ * observation of the new acting seat. Buffers and values_capacity as in the
+ * calls above (with a small capacity the step is applied, counts / offsets /
+ * mask are written and JQ_E_CAPACITY comes back before values and the
+ * observation). hash: device uint64 (N), each env's Zobrist hash after its ply
+ * and before any restart; terminated / reward as jq_step's; actions_out the
+ * action taken (world id, -1 none). */
+int jq_env_step(jq_env *env, const int32_t *actions, int32_t sampler, uint64_t sample_seed, uint64_t ply,
+                int64_t reset_seed, int32_t *counts, int32_t *offsets, int32_t *values, int64_t values_capacity,
                 int32_t *mask_words, int32_t obs_fmt, void *spatial, float *aux, float *global,
-                uint8_t *terminated, float *reward, int32_t *actions_out, void *stream);
+                uint8_t *terminated, float *reward, uint64_t *hash, int32_t *actions_out, void *stream);
 
 /* State import / export (host memory), one field at a time. Replaces
  * DeviceGameStateBatch.copy_to_host / copy_from_host (bindings.cpp:73-198).
@@ -234,6 +285,10 @@ int jq_field_ptr(jq_env *env, int32_t field, void **dev_ptr, int64_t *env_stride
  * (through jq_set_field or a jq_field_ptr view) reach observations only after
  * this call or jq_rehash. */
 int jq_finalize_import(jq_env *env, void *stream);
+/* jq_finalize_import restricted to the envs whose env_mask (device uint8, N)
+ * entry is nonzero; the others keep their hash, beliefs and summaries.
+ * Synchronises. */
+int jq_finalize_import_masked(jq_env *env, const uint8_t *env_mask, void *stream);
 /* Recompute every env's Zobrist hash and combat-memory summaries from its
  * current fields (after editing scalar fields such as the termination flags);
  * beliefs are left as they are. */

@@ -12,6 +12,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libjunqi_amd.so"
 
 JQ_OK = 0
+JQ_E_ARG, JQ_E_STATE, JQ_E_HIP, JQ_E_OOM, JQ_E_CAPACITY = -1, -2, -3, -4, -5
+SAMPLE_UNIFORM, SAMPLE_LOGITS = 0, 1
 OBS_F32, OBS_BF16, OBS_U8 = 0, 1, 2
 ACT_WORLD, ACT_CANONICAL = 0, 1
 NUM_CELLS = 289
@@ -41,8 +43,9 @@ _EXPORTS = [
     "jq_last_error", "jq_version", "jq_create", "jq_destroy", "jq_num_envs", "jq_upload_zobrist",
     "jq_upload_recency", "jq_upload_setup_pool", "jq_reset_lineups", "jq_reset_seeded",
     "jq_generate_lineups", "jq_generate_pool", "jq_generate_styled", "jq_board_tables", "jq_reset_terminated", "jq_step",
-    "jq_legal", "jq_legal_slots", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_env_step",
-    "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import", "jq_rehash",
+    "jq_legal", "jq_legal_slots", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_sample_logits",
+    "jq_env_step", "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import",
+    "jq_finalize_import_masked", "jq_rehash", "jq_validate_lineup",
     "jq_sync", "jq_history_create", "jq_history_destroy", "jq_history_bytes", "jq_history_snapshot",
     "jq_history_reconstruct", "jq_mask_count", "jq_mask_to_ids", "jq_ids_to_mask", "jq_upload_beliefs",
     "jq_clear_beliefs",
@@ -51,6 +54,15 @@ _EXPORTS = [
 
 class JunqiError(RuntimeError):
     """A C-ABI call returned an error code."""
+
+
+class ArgumentError(JunqiError, ValueError):
+    """A call was given a bad argument (JQ_E_ARG): also a ValueError, which the
+    reference raises for invalid setups and seats."""
+
+
+class CapacityError(JunqiError):
+    """An output buffer was smaller than the result (JQ_E_CAPACITY)."""
 
 
 def _load() -> C.CDLL:
@@ -75,16 +87,19 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_generate_styled": ([I32, I64, I32, I32, C.c_char_p, I32, P], C.c_int), "jq_board_tables": ([P, I64], C.c_int),
         "jq_reset_terminated": ([P, I64, P], C.c_int),
         "jq_step": ([P, P, P, I32, P, P, P, P, P, P, P, P, P, P], C.c_int),
-        "jq_legal": ([P, P, P, P, P, P, P, P], C.c_int),
+        "jq_legal": ([P, P, P, P, P, I64, P, P, P], C.c_int),
         "jq_legal_slots": ([P, P, P, P], C.c_int),
         "jq_observe": ([P, P, I32, I32, P, P, P, P], C.c_int),
         "jq_obs_decode_table": ([P], C.c_int),
-        "jq_sample_uniform": ([P, P, P, P, U64, U64, P, P], C.c_int),
-        "jq_env_step": ([P, P, U64, U64, I64, P, P, P, P, I32, P, P, P, P, P, P, P], C.c_int),
+        "jq_sample_uniform": ([P, P, P, P, I64, U64, U64, P, P], C.c_int),
+        "jq_sample_logits": ([P, P, P, P, P, I64, U64, U64, P, P, P], C.c_int),
+        "jq_env_step": ([P, P, I32, U64, U64, I64, P, P, P, I64, P, I32, P, P, P, P, P, P, P, P], C.c_int),
+        "jq_validate_lineup": ([P], C.c_int),
         "jq_field_info": ([I32, C.POINTER(I32), C.POINTER(I32)], C.c_int),
         "jq_get_field": ([P, I32, P], C.c_int), "jq_set_field": ([P, I32, P], C.c_int),
         "jq_field_ptr": ([P, I32, C.POINTER(P), C.POINTER(I64), C.POINTER(I64)], C.c_int),
-        "jq_finalize_import": ([P, P], C.c_int), "jq_rehash": ([P, P], C.c_int),
+        "jq_finalize_import": ([P, P], C.c_int), "jq_finalize_import_masked": ([P, P, P], C.c_int),
+        "jq_rehash": ([P, P], C.c_int),
         "jq_sync": ([P], C.c_int),
         "jq_history_create": ([C.POINTER(P), I32, I32, I32, I32], C.c_int),
         "jq_history_destroy": ([P], C.c_int), "jq_history_bytes": ([P, C.POINTER(I64)], C.c_int),
@@ -105,8 +120,15 @@ lib = _load()
 
 
 def check(rc: int) -> None:
+    """Raise for a failed call: ArgumentError (a ValueError) for bad arguments,
+    CapacityError for a too small output buffer, JunqiError otherwise."""
     if rc != JQ_OK:
-        raise JunqiError(f"junqi_amd error {rc}: {lib.jq_last_error().decode()}")
+        msg = f"junqi_amd error {rc}: {lib.jq_last_error().decode()}"
+        if rc == JQ_E_ARG:
+            raise ArgumentError(msg)
+        if rc == JQ_E_CAPACITY:
+            raise CapacityError(msg)
+        raise JunqiError(msg)
 
 
 def exported_symbols() -> list[str]:

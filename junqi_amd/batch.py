@@ -185,7 +185,8 @@ class JunqiBatch:
         p = self._ptr
         check(lib.jq_legal(self._h, p(s), self.counts.data_ptr(),
                            self.offsets.data_ptr() if csr else None, self.values.data_ptr() if csr else None,
-                           self.mask_words.data_ptr() if mask_words else None, p(mb), self.stream))
+                           self.values.numel(), self.mask_words.data_ptr() if mask_words else None, p(mb),
+                           self.stream))
         out = {"counts": self.counts}
         if csr:
             out["offsets"] = self.offsets
@@ -262,23 +263,41 @@ class JunqiBatch:
 
     # ------------------------------------------------------------ sampling / fused step
     def sample_uniform(self, seed: int, ply: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """World action per env, uniform over the current CSR rows (Philox)."""
         if out is None:
             out = torch.empty(self.n, dtype=torch.int32, device=self.device)
         check(lib.jq_sample_uniform(self._h, self.counts.data_ptr(), self.offsets.data_ptr(),
-                                    self.values.data_ptr(), int(seed), int(ply), out.data_ptr(), self.stream))
+                                    self.values.data_ptr(), self.values.numel(), int(seed), int(ply),
+                                    out.data_ptr(), self.stream))
         return out
 
-    def env_step(self, *, actions: torch.Tensor | None = None, sample_seed: int = 0, ply: int = 0,
-                 reset_seed: int = 0, obs_fmt: str = "u8", spatial: torch.Tensor | None = None,
+    def sample_logits(self, seed: int, ply: int, acting: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None, canonical_out: torch.Tensor | None = None) -> torch.Tensor:
+        """World action per env: argmax of i.i.d. N(0,1) logits (Philox) over the
+        acting seat's legal canonical ids of the current CSR rows."""
+        if out is None:
+            out = torch.empty(self.n, dtype=torch.int32, device=self.device)
+        s = None if acting is None else acting.to(device=self.device, dtype=torch.int8).contiguous()
+        check(lib.jq_sample_logits(self._h, self._ptr(s), self.counts.data_ptr(), self.offsets.data_ptr(),
+                                   self.values.data_ptr(), self.values.numel(), int(seed), int(ply),
+                                   out.data_ptr(), self._ptr(canonical_out), self.stream))
+        return out
+
+    def env_step(self, *, actions: torch.Tensor | None = None, sampler: str = "uniform", sample_seed: int = 0,
+                 ply: int = 0, reset_seed: int = 0, obs_fmt: str = "u8", spatial: torch.Tensor | None = None,
                  aux: torch.Tensor | None = None, glob: torch.Tensor | None = None,
                  terminated: torch.Tensor | None = None, reward: torch.Tensor | None = None,
-                 actions_out: torch.Tensor | None = None) -> None:
+                 hash_out: torch.Tensor | None = None, actions_out: torch.Tensor | None = None) -> None:
+        """One fused env-step (jq_env_step): sample from the current CSR rows
+        unless `actions` are given (sampler "uniform" or "logits"), step,
+        restart finished games from the pool, next legal sets, observation."""
         code = {"f32": L.OBS_F32, "bf16": L.OBS_BF16, "u8": L.OBS_U8}[obs_fmt]
+        smp = {"uniform": L.SAMPLE_UNIFORM, "logits": L.SAMPLE_LOGITS}[sampler]
         p = self._ptr
-        check(lib.jq_env_step(self._h, p(actions), int(sample_seed), int(ply), int(reset_seed),
+        check(lib.jq_env_step(self._h, p(actions), smp, int(sample_seed), int(ply), int(reset_seed),
                               self.counts.data_ptr(), self.offsets.data_ptr(), self.values.data_ptr(),
-                              self.mask_words.data_ptr(), code, p(spatial), p(aux), p(glob), p(terminated),
-                              p(reward), p(actions_out), self.stream))
+                              self.values.numel(), self.mask_words.data_ptr(), code, p(spatial), p(aux), p(glob),
+                              p(terminated), p(reward), p(hash_out), p(actions_out), self.stream))
 
     # ------------------------------------------------------------ state import / export
     def get_field(self, name: str) -> np.ndarray:
@@ -305,25 +324,20 @@ class JunqiBatch:
         check(lib.jq_rehash(self._h, self.stream))
         torch.cuda.synchronize(self.device)
 
-    def import_state(self, sd: dict, *, terminated=None, winner_team=None, draw=None,
-                     move_history=None) -> None:
-        """Load every env from the flat SoA dict that the reference's
-        ``DeviceGameStateBatch.copy_from_host`` takes (keys of
-        junqi_rl/gpu_rollout.py:448-483: per-piece arrays of N*120, cell_piece_id
-        of N*289, seat arrays of N*4, per-env turn / move_counter /
-        moves_since_last_combat). Combat memory starts empty and beliefs are
-        re-seeded from the board, as GameState.__post_init__ does for a state
-        built from arrays (state.py:346-483); the Zobrist hash is recomputed.
-        move_history: optional list (one per env) of (src_flat, dst_flat)
-        pairs, most recent last."""
+    def _fields_from_dict(self, sd: dict) -> dict[str, np.ndarray]:
+        """This handle's per-env fields from the flat SoA dict of the reference's
+        DeviceGameStateBatch.copy_from_host (bindings.cpp:73-112; the keys of
+        junqi_rl/gpu_rollout.py:447-483): per-piece arrays of N*120,
+        cell_piece_id of N*289, seat arrays of N*4, per-env turn / move_counter /
+        moves_since_last_combat. Missing keys raise KeyError, wrong sizes ValueError."""
         n = self.n
 
         def arr(key, shape, dt):
             if key not in sd:
-                raise KeyError(f"import_state: missing key {key!r}")
+                raise KeyError(f"state dict: missing key {key!r}")
             a = np.asarray(sd[key])
             if a.size != int(np.prod(shape)):
-                raise ValueError(f"import_state: {key} has {a.size} elements, expected {int(np.prod(shape))}")
+                raise ValueError(f"state dict: {key} has {a.size} elements, expected {int(np.prod(shape))}")
             return a.reshape(shape).astype(dt, copy=False)
 
         alive = arr("alive", (n, 120), bool)
@@ -338,26 +352,51 @@ class JunqiBatch:
             return out
         cell = np.full((n, 292), -1, np.int8)
         cell[:, :289] = cpid
-        self.set_field("cell", cell)
-        self.set_field("ptype", pid128(np.where(ptype > 0, ptype, -1), -1, np.int8))
-        self.set_field("pos", pid128(np.where(alive & (px >= 0) & (py >= 0), py * 17 + px, -1), -1, np.int16))
-        self.set_field("zero", pid128(np.where((zx >= 0) & (zy >= 0), zy * 17 + zx, -1), -1, np.int16))
+        bits = np.arange(4, dtype=np.uint8)
+        f = {
+            "cell": cell,
+            "ptype": pid128(np.where(ptype > 0, ptype, -1), -1, np.int8),
+            "pos": pid128(np.where(alive & (px >= 0) & (py >= 0), py * 17 + px, -1), -1, np.int16),
+            "zero": pid128(np.where((zx >= 0) & (zy >= 0), zy * 17 + zx, -1), -1, np.int16),
+            "death_reason": pid128(arr("death_reason_arr", (n, 120), np.int8), -1, np.int8),
+            "death_step": pid128(arr("death_step_arr", (n, 120), np.int16), -1, np.int16),
+            "death_loc": pid128(arr("death_loc_flat_arr", (n, 120), np.int16), -1, np.int16),
+            "seat_dead": (arr("seat_dead_arr", (n, 4), np.uint8) << bits).sum(-1).astype(np.uint8).reshape(n, 1),
+            "flag_rev": (arr("seat_flag_revealed_arr", (n, 4), np.uint8) << bits).sum(-1).astype(np.uint8).reshape(n, 1),
+            "turn": arr("turn", (n,), np.int8).reshape(n, 1),
+            "move_counter": arr("move_counter", (n,), np.int32).reshape(n, 1),
+            "mslc": arr("moves_since_last_combat", (n,), np.int32).reshape(n, 1),
+        }
         for ours, key in (("move_count", "move_count_arr"), ("active_eat", "active_eat_arr"),
                           ("passive_surv", "passive_surv_arr")):
-            self.set_field(ours, pid128(arr(key, (n, 120), np.int16), 0, np.int16))
-        self.set_field("death_reason", pid128(arr("death_reason_arr", (n, 120), np.int8), -1, np.int8))
-        self.set_field("death_step", pid128(arr("death_step_arr", (n, 120), np.int16), -1, np.int16))
-        self.set_field("death_loc", pid128(arr("death_loc_flat_arr", (n, 120), np.int16), -1, np.int16))
-        for name in _CM_FIELDS:
+            f[ours] = pid128(arr(key, (n, 120), np.int16), 0, np.int16)
+        return f
+
+    def _clear_history_and_memory(self, rows: np.ndarray | None = None) -> None:
+        """Empty combat memory and move history for the envs in `rows` (bool N; all when None)."""
+        n = self.n
+        for name in _CM_FIELDS + ("hist", "hist_meta"):
             e, _ = L.field_info(name)
             fill = -1 if name in ("cm_last_direct", "cm_last_chain", "cm_floor_step") else 0
-            self.set_field(name, np.full((n, e), fill, np.int64))
-        bits = np.arange(4, dtype=np.uint8)
-        self.set_field("seat_dead", (arr("seat_dead_arr", (n, 4), np.uint8) << bits).sum(-1).astype(np.uint8))
-        self.set_field("flag_rev", (arr("seat_flag_revealed_arr", (n, 4), np.uint8) << bits).sum(-1).astype(np.uint8))
-        self.set_field("turn", arr("turn", (n,), np.int8))
-        self.set_field("move_counter", arr("move_counter", (n,), np.int32))
-        self.set_field("mslc", arr("moves_since_last_combat", (n,), np.int32))
+            if rows is None:
+                self.set_field(name, np.full((n, e), fill, np.int64))
+            else:
+                cur = self.get_field(name)
+                cur[rows] = fill
+                self.set_field(name, cur)
+
+    def import_state(self, sd: dict, *, terminated=None, winner_team=None, draw=None,
+                     move_history=None) -> None:
+        """Load every env from the flat SoA dict that the reference's
+        ``DeviceGameStateBatch.copy_from_host`` takes (see _fields_from_dict).
+        Combat memory starts empty and beliefs are re-seeded from the board, as
+        GameState.__post_init__ does for a state built from arrays
+        (state.py:346-483); the Zobrist hash is recomputed. move_history:
+        optional list (one per env) of (src_flat, dst_flat) pairs, most recent last."""
+        n = self.n
+        for name, v in self._fields_from_dict(sd).items():
+            self.set_field(name, v)
+        self._clear_history_and_memory()
         hist = np.zeros((n, 32), np.int32)
         meta = np.zeros((n, 1), np.int32)
         for i, h in enumerate(move_history or []):
@@ -371,6 +410,89 @@ class JunqiBatch:
                              np.full(n, -1, np.int8) if winner_team is None else winner_team,
                              np.zeros(n, bool) if draw is None else draw, finalize=False)
         self.finalize_import()
+
+    # ---------------------------------------------- DeviceGameStateBatch host copies
+    # The host round trip of the reference's device state (bindings.cpp:73-243)
+    # as the v1 PPO collector drives it through GpuRollout.state
+    # (junqi_rl/training/gpu_collector.py:375, 538, 602-650).
+    def copy_turn_to_host(self) -> np.ndarray:
+        """(N,) int8 acting seat per env (py_copy_turn_to_host, bindings.cpp:186-194)."""
+        return self.get_field("turn")[:, 0].astype(np.int8)
+
+    def copy_to_host(self) -> dict[str, np.ndarray]:
+        """The 21 flat arrays of py_copy_to_host (bindings.cpp:117-183), keys and
+        dtypes as there: per-piece arrays N*120, cell_piece_id N*289, seat flags
+        N*4, turn / zobrist / move_counter / moves_since_last_combat N."""
+        n = self.n
+        pos = self.get_field("pos")[:, :120].astype(np.int16)
+        alive = pos >= 0
+        ptype = self.get_field("ptype")[:, :120].astype(np.int8)
+        zero = self.get_field("zero")[:, :120].astype(np.int16)
+        seat = np.where(ptype >= 0, np.arange(120, dtype=np.int8)[None, :] // 30, np.int8(-1)).astype(np.int8)
+        bits = np.arange(4, dtype=np.uint8)
+        flat = lambda a: np.ascontiguousarray(a).reshape(-1)  # noqa: E731
+        return {
+            "cell_piece_id_per_piece": flat(np.where(alive, pos, -1).astype(np.int16)),
+            "piece_seat_arr": flat(seat),
+            "piece_type_arr": flat(ptype),
+            "alive": flat(alive),
+            "pos_x": flat(np.where(alive, pos % 17, -1).astype(np.int8)),
+            "pos_y": flat(np.where(alive, pos // 17, -1).astype(np.int8)),
+            "zero_x": flat(np.where(zero >= 0, zero % 17, -1).astype(np.int8)),
+            "zero_y": flat(np.where(zero >= 0, zero // 17, -1).astype(np.int8)),
+            "move_count_arr": flat(self.get_field("move_count")[:, :120].astype(np.int16)),
+            "active_eat_arr": flat(self.get_field("active_eat")[:, :120].astype(np.int16)),
+            "passive_surv_arr": flat(self.get_field("passive_surv")[:, :120].astype(np.int16)),
+            "death_reason_arr": flat(self.get_field("death_reason")[:, :120].astype(np.int8)),
+            "death_step_arr": flat(self.get_field("death_step")[:, :120].astype(np.int16)),
+            "death_loc_flat_arr": flat(self.get_field("death_loc")[:, :120].astype(np.int16)),
+            "cell_piece_id": flat(self.get_field("cell")[:, :289].astype(np.int16)),
+            "seat_dead_arr": flat(((self.get_field("seat_dead")[:, :1] >> bits) & 1).astype(bool)),
+            "seat_flag_revealed_arr": flat(((self.get_field("flag_rev")[:, :1] >> bits) & 1).astype(bool)),
+            "turn": flat(self.get_field("turn")[:, 0].astype(np.int8)),
+            "zobrist": flat(self.get_field("zobrist")[:, 0].view(np.int64)),
+            "move_counter": flat(self.get_field("move_counter")[:, 0].astype(np.int32)),
+            "moves_since_last_combat": flat(self.get_field("mslc")[:, 0].astype(np.int32)),
+        }
+
+    def copy_from_host(self, sd: dict) -> None:
+        """Write the copy_to_host dict back (py_copy_from_host, bindings.cpp:73-112).
+        Envs whose position the dict leaves as it is keep everything; an env
+        whose fields it changes (the v1 collector writes fresh games into reset
+        slots, gpu_collector.py:596-643) starts from the imported position as a
+        GameState built from arrays does (state.py:346-483): empty combat memory
+        and move history, beliefs seeded from the board, the Zobrist hash
+        recomputed from the fields (the dict's zobrist is not read)."""
+        n = self.n
+        new = self._fields_from_dict(sd)
+        cur = {k: self.get_field(k) for k in new}
+        width = {k: (289 if k == "cell" else 120 if v.shape[1] == 128 else v.shape[1]) for k, v in new.items()}
+        changed = np.zeros(n, bool)
+        for k, v in new.items():   # padding columns (pids 120-127, cells 289-291) are the handle's own
+            w = width[k]
+            changed |= (cur[k].reshape(n, -1)[:, :w] != v.reshape(n, -1)[:, :w]).any(axis=1)
+        if not changed.any():
+            return
+        for k, v in new.items():
+            merged = cur[k].reshape(n, -1).copy()
+            w = width[k]
+            merged[changed, :w] = v.reshape(n, -1)[changed, :w]
+            self.set_field(k, merged)
+        self._clear_history_and_memory(changed)
+        mask = torch.from_numpy(changed.astype(np.uint8)).to(self.device)
+        check(lib.jq_finalize_import_masked(self._h, mask.data_ptr(), self.stream))
+
+    def copy_termination_to_host(self) -> dict[str, np.ndarray]:
+        """terminated / winner_team / draw (py_copy_termination_to_host, bindings.cpp:216-231)."""
+        return self.termination()
+
+    def copy_termination_from_host(self, terminated, winner_team, draw) -> None:
+        """py_copy_termination_from_host (bindings.cpp:201-214); hashes follow."""
+        for name, a in (("terminated", terminated), ("winner_team", winner_team), ("draw", draw)):
+            if np.asarray(a).size != self.n:
+                raise ValueError(f"{name} size mismatch")
+        self.set_termination(terminated, winner_team, draw)
+        torch.cuda.synchronize(self.device)
 
     def set_termination(self, terminated, winner_team, draw, *, finalize: bool = True) -> None:
         """Overwrite the per-env terminated / winner_team / draw flags

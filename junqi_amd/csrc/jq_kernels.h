@@ -471,6 +471,7 @@ __device__ __forceinline__ bool sees_truth(int o, int owner, int mode)
 struct StepOut {
     uint8_t *valid; int8_t *event; uint8_t *term; int8_t *winner; uint8_t *draw;
     uint8_t *fcap; uint8_t *died; float *reward; int32_t *world;
+    uint64_t *hash;   // Zobrist hash after the ply (unchanged when none was applied)
 };
 
 // Kill pid at its current cell (state.py:1027-1049). Uniform; lane 0 stores.
@@ -671,6 +672,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
         if (O.died) O.died[env] = 0;
         if (O.reward) O.reward[env] = 0.f;
         if (O.world) O.world[env] = -1;
+        if (O.hash) O.hash[env] = E.zob;
     }
     if (was_term) return;
 
@@ -805,6 +807,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
         if (O.fcap) O.fcap[env] = fcap;
         if (O.died) O.died[env] = (uint8_t)died;
         if (O.reward) O.reward[env] = (term && !drw && win >= 0) ? (((seat & 1) == win) ? 1.f : -1.f) : 0.f;
+        if (O.hash) O.hash[env] = zob;
     }
 }
 
@@ -955,11 +958,11 @@ __global__ __launch_bounds__(64) void k_reset_terminated(State S, int64_t seed)
 }
 
 // Recompute Zobrist and (if `beliefs`) re-seed beliefs from the current board
-// (hand-built states).
-__global__ __launch_bounds__(64) void k_finalize(State S, int beliefs)
+// (hand-built states); only envs whose `mask` entry is nonzero when a mask is given.
+__global__ __launch_bounds__(64) void k_finalize(State S, int beliefs, const uint8_t *__restrict__ mask)
 {
     const int env = blockIdx.x, l = threadIdx.x;
-    if (env >= S.n) return;
+    if (env >= S.n || (mask && !mask[env])) return;
     uint64_t z = 0;
     for (int p = l; p < NP; p += 64) {
         const size_t pi = (size_t)env * PID_STRIDE + p;
@@ -1259,7 +1262,8 @@ __device__ __forceinline__ int select64(uint64_t x, int k)
 // ...: it finds its piece from the running counts, the destination by selecting
 // a bit of that piece's mask, and maps it to a flat cell through an LDS copy of
 // the compact table.
-__global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict__ offsets, int32_t *__restrict__ values)
+__global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict__ offsets, int32_t *__restrict__ values,
+                                             int64_t cap)
 {
     const int l = threadIdx.x, h = l >> 5, p = l & 31;
     const int env = 2 * (int)blockIdx.x + h;
@@ -1292,7 +1296,7 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
             if (j + step < n && start[h][j + step] <= i) j += step;
         const uint64_t w0 = __shfl(m0, j, 32), w1 = __shfl(m1, j, 32), w2 = __shfl(m2, j, 32);
         const int s = __shfl(src, j, 32);
-        if (i < total) {
+        if (i < total && (int64_t)base + i < cap) {
             const int k = i - start[h][j];
             const int c0 = __popcll(w0), c1 = __popcll(w1);
             const int c = k < c0 ? select64(w0, k)
@@ -1402,25 +1406,85 @@ __device__ __forceinline__ uint32_t philox4x32_10(uint32_t c0, uint32_t c1, uint
 
 // Uniform pick from env's CSR row: Philox4x32-10 word 0 of counter
 // (env, ply lo, ply hi, 0) under key (seed lo, seed hi), scaled to the count;
-// -1 for an empty row.
+// -1 for an empty row or one that does not lie inside the values buffer.
 __device__ __forceinline__ int32_t sample_pick(int env, const int32_t *__restrict__ counts,
                                                const int32_t *__restrict__ offsets, const int32_t *__restrict__ values,
-                                               uint64_t seed, uint64_t ply)
+                                               int64_t cap, uint64_t seed, uint64_t ply)
 {
     const int c = counts[env];
     if (c <= 0) return -1;
+    const int64_t off = offsets[env];
+    if (off < 0 || off + c > cap) return -1;
     const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
                                      (uint32_t)seed, (uint32_t)(seed >> 32));
     const int idx = (int)(((uint64_t)u * (uint64_t)c) >> 32);
-    return values[offsets[env] + idx];
+    return values[off + idx];
 }
 
 __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
-                         const int32_t *__restrict__ values, uint64_t seed, uint64_t ply, int32_t *__restrict__ out)
+                         const int32_t *__restrict__ values, int64_t cap, uint64_t seed, uint64_t ply,
+                         int32_t *__restrict__ out)
 {
     const int env = blockIdx.x * blockDim.x + threadIdx.x;
     if (env >= n) return;
-    out[env] = sample_pick(env, counts, offsets, values, seed, ply);
+    out[env] = sample_pick(env, counts, offsets, values, cap, seed, ply);
+}
+
+// Masked-logit pick by env's wave (lane l): the legal ids of the CSR row, lane
+// j taking ids j, j + 64, ...; each id's canonical id c under `seat` draws
+// u_c = Philox word 0 of counter (env, ply lo, ply hi, 1 + c). The N(0,1) logit
+// Phi^-1((u_c + 1/2) / 2^32) is increasing in u_c, so the argmax over the row is
+// the largest u_c, ties to the smallest c: one 64-bit key (u_c, ~c) per lane,
+// maximised across the wave. Returns the world id (wave-uniform, -1 for an
+// empty or out-of-buffer row) and its canonical id in `canon`.
+__device__ __forceinline__ int32_t sample_logits_wave(int env, int l, int seat, const int32_t *__restrict__ counts,
+                                                      const int32_t *__restrict__ offsets,
+                                                      const int32_t *__restrict__ values, int64_t cap, uint64_t seed,
+                                                      uint64_t ply, int &canon)
+{
+    canon = -1;
+    const int c = counts[env];
+    if (c <= 0 || seat < 0 || seat > 3) return -1;
+    const int64_t off = offsets[env];
+    if (off < 0 || off + c > cap) return -1;
+    uint64_t best = 0;
+    int32_t bw = -1;
+    for (int j = l; j < c; j += 64) {
+        const int32_t w = values[off + j];
+        const int src = w / NC, dst = w - src * NC;
+        const int cc = (int)cT.rotc[seat][cT.f2c[src]] * NONB + (int)cT.rotc[seat][cT.f2c[dst]];
+        const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), (uint32_t)(1 + cc),
+                                         (uint32_t)seed, (uint32_t)(seed >> 32));
+        const uint64_t key = ((uint64_t)u << 32) | (uint32_t)~(uint32_t)cc;   // > 0 for every real id
+        if (key > best) { best = key; bw = w; }
+    }
+    uint64_t m = best;
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t v = __shfl_xor(m, o);
+        m = v > m ? v : m;
+    }
+    const uint64_t who = __ballot(best == m && bw >= 0);
+    const int src_lane = who ? __builtin_ctzll(who) : 0;
+    canon = (int)~(uint32_t)(m & 0xFFFFFFFFu);
+    return __shfl(bw, src_lane);
+}
+
+__global__ __launch_bounds__(64) void k_sample_logits(State S, const int8_t *__restrict__ acting,
+                                                      const int32_t *__restrict__ counts,
+                                                      const int32_t *__restrict__ offsets,
+                                                      const int32_t *__restrict__ values, int64_t cap, uint64_t seed,
+                                                      uint64_t ply, int32_t *__restrict__ out,
+                                                      int32_t *__restrict__ canon_out)
+{
+    const int env = blockIdx.x, l = threadIdx.x;
+    if (env >= S.n) return;
+    const int seat = acting ? acting[env] : S.env[env].turn;
+    int cc;
+    const int32_t a = sample_logits_wave(env, l, seat, counts, offsets, values, cap, seed, ply, cc);
+    if (l == 0) {
+        out[env] = a;
+        if (canon_out) canon_out[env] = a >= 0 ? cc : -1;
+    }
 }
 
 // One env-step's state work by one wave per env: the action (given, or the
@@ -1445,8 +1509,8 @@ struct EnvLds {
 // Philox pick from the env's previous CSR row `offsets` / `values` with
 // `counts`), the pool restart and the outputs.
 struct EnvStepArgs {
-    const int32_t *actions; uint64_t sample_seed, ply; const int32_t *offsets, *values;
-    int32_t *actions_out; StepOut O; int do_reset; int64_t reset_seed;
+    const int32_t *actions; int sampler; uint64_t sample_seed, ply; const int32_t *offsets, *values;
+    int64_t values_cap; int32_t *actions_out; StepOut O; int do_reset; int64_t reset_seed;
     int32_t *counts, *mask_words;
 };
 
@@ -1456,8 +1520,16 @@ struct EnvStepArgs {
 // only its own wave (wave_sync), so it never waits on other waves of a block.
 __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, const EnvStepArgs &A, EnvLds &E)
 {
-    const int32_t a = A.actions ? A.actions[env]
-                                : sample_pick(env, A.counts, A.offsets, A.values, A.sample_seed, A.ply);
+    int32_t a;
+    if (A.actions) {
+        a = A.actions[env];
+    } else if (A.sampler == 1) {
+        int cc;
+        a = sample_logits_wave(env, l, S.env[env].turn, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed,
+                               A.ply, cc);
+    } else {
+        a = sample_pick(env, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed, A.ply);
+    }
     if (A.actions_out && l == 0) A.actions_out[env] = a;
     TurnAfter nx;
     step_env(S, env, l, a, nullptr, 0, A.O, E.cell, E.pos, E.ptype, nx);

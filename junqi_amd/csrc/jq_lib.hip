@@ -30,6 +30,9 @@ struct jq_env {
     int obs_blocks = 0;              // resident u8 observation blocks on the device
     float *ext_bel = nullptr;        // uploaded (N, 4, 12, 289) beliefs, allocated on first upload
     bool ext_on = false;             // observations read the uploaded beliefs
+    int8_t *pool = nullptr;          // setup pool buffer (reused while uploads fit)
+    int32_t pool_cap = 0;            // entries the pool buffer holds
+    int32_t *total_host = nullptr;   // pinned host word for CSR totals read back
 };
 
 // Rollout history: per-step copies of every per-env state block.
@@ -195,6 +198,41 @@ uint8_t *field_array(jq_env *e, int arr)
 
 inline hipStream_t strm(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// validate_setup (setup.py:139-159) of `count` setups of 120 slot types: the
+// first seat lineup that breaks C1-C5 fails the call with its rules named.
+int check_setups(const int8_t *host, size_t count, const char *what)
+{
+    static const char *kRule[6] = {"TYPE", "C1", "C2", "C3", "C4", "C5"};
+    for (size_t i = 0; i < count; ++i)
+        for (int seat = 0; seat < 4; ++seat) {
+            const int v = validate_lineup(host + i * NP + 30 * seat);
+            if (!v) continue;
+            std::string names;
+            for (int b = 0; b < 6; ++b)
+                if (v & (1 << b)) names += std::string(names.empty() ? "" : ",") + kRule[b];
+            return fail(JQ_E_ARG, "setup violates rules: %s %zu seat %d breaks %s", what, i, seat, names.c_str());
+        }
+    return JQ_OK;
+}
+
+// CSR capacity check of jq_legal / jq_env_step: with a values buffer smaller
+// than N * JQ_MAX_LEGAL the total (offsets[n], just scanned on `s`) is read back
+// and must fit.
+int csr_fits(jq_env *e, const int32_t *offsets, int64_t cap, hipStream_t s)
+{
+    if (cap >= (int64_t)e->S.n * JQ_MAX_LEGAL) return JQ_OK;
+    if (!e->total_host) {
+        void *q = nullptr;
+        if (hipHostMalloc(&q, sizeof(int32_t)) != hipSuccess) return fail(JQ_E_OOM, "pinned host word");
+        e->total_host = static_cast<int32_t *>(q);
+    }
+    HIP_TRY(hipMemcpyAsync(e->total_host, offsets + e->S.n, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if ((int64_t)*e->total_host > cap)
+        return fail(JQ_E_CAPACITY, "legal ids need %d values, the buffer holds %lld", *e->total_host, (long long)cap);
+    return JQ_OK;
+}
+
 int check_env(jq_env *e)
 {
     if (!e) return fail(JQ_E_ARG, "null handle");
@@ -274,6 +312,8 @@ int jq_destroy(jq_env *e)
     (void)hipSetDevice(e->device);
 
     for (void *p : e->allocs) (void)hipFree(p);
+    if (e->pool) (void)hipFree(e->pool);
+    if (e->total_host) (void)hipHostFree(e->total_host);
     delete e;
     return JQ_OK;
 }
@@ -300,15 +340,30 @@ int jq_upload_recency(jq_env *e, const float *host)
     return JQ_OK;
 }
 
+int jq_validate_lineup(const int8_t *lineup30)
+{
+    if (!lineup30) return fail(JQ_E_ARG, "null lineup");
+    return validate_lineup(lineup30);
+}
+
 int jq_upload_setup_pool(jq_env *e, const int8_t *host, int32_t pool_size)
 {
     int rc = check_env(e);
     if (rc) return rc;
     if (!host || pool_size <= 0) return fail(JQ_E_ARG, "empty setup pool");
-    int8_t *p = nullptr;
-    if ((rc = dalloc(e, p, (size_t)pool_size * NP, 0)) != 0) return rc;
-    HIP_TRY(hipMemcpy(p, host, (size_t)pool_size * NP, hipMemcpyHostToDevice));
-    e->S.pool = p;
+    if ((rc = check_setups(host, (size_t)pool_size, "pool entry")) != 0) return rc;
+    // kernels of any stream may still read the old pool: let them finish first
+    HIP_TRY(hipDeviceSynchronize());
+    if (pool_size > e->pool_cap) {
+        if (e->pool) { (void)hipFree(e->pool); e->pool = nullptr; e->pool_cap = 0; e->S.pool = nullptr; e->S.pool_size = 0; }
+        void *q = nullptr;
+        if (hipMalloc(&q, (size_t)pool_size * NP) != hipSuccess)
+            return fail(JQ_E_OOM, "hipMalloc(%zu) for the setup pool failed", (size_t)pool_size * NP);
+        e->pool = static_cast<int8_t *>(q);
+        e->pool_cap = pool_size;
+    }
+    HIP_TRY(hipMemcpy(e->pool, host, (size_t)pool_size * NP, hipMemcpyHostToDevice));
+    e->S.pool = e->pool;
     e->S.pool_size = pool_size;
     return JQ_OK;
 }
@@ -319,6 +374,7 @@ int jq_reset_lineups(jq_env *e, const int8_t *host, void *stream)
     if (rc) return rc;
     if (!host) return fail(JQ_E_ARG, "null lineups");
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before resetting");
+    if ((rc = check_setups(host, (size_t)e->S.n, "env")) != 0) return rc;
     int8_t *d = nullptr;
     const size_t bytes = (size_t)e->S.n * NP;
     HIP_TRY(hipMallocAsync((void **)&d, bytes, strm(stream)));
@@ -397,18 +453,19 @@ int jq_step(jq_env *e, const int32_t *actions, const int8_t *acting, int32_t fmt
     if (!actions) return fail(JQ_E_ARG, "null actions");
     if (fmt != JQ_ACT_WORLD && fmt != JQ_ACT_CANONICAL) return fail(JQ_E_ARG, "bad action format %d", fmt);
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before stepping");
-    StepOut O{valid, event, terminated, winner, draw, flag_captured, seats_died, reward, world_action};
+    StepOut O{valid, event, terminated, winner, draw, flag_captured, seats_died, reward, world_action, nullptr};
     hipLaunchKernelGGL(k_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, actions, acting, fmt, O);
     return launch_check("k_step");
 }
 
 int jq_legal(jq_env *e, const int8_t *acting, int32_t *counts, int32_t *offsets, int32_t *values,
-             int32_t *mask_words, uint8_t *mask_bool, void *stream)
+             int64_t values_capacity, int32_t *mask_words, uint8_t *mask_bool, void *stream)
 {
     int rc = check_env(e);
     if (rc) return rc;
     if ((offsets || values) && !counts) return fail(JQ_E_ARG, "offsets/values need counts");
     if (values && !offsets) return fail(JQ_E_ARG, "values need offsets");
+    if (values && values_capacity < 0) return fail(JQ_E_ARG, "negative values capacity");
     hipLaunchKernelGGL(k_legal, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, acting, counts, mask_words, mask_bool);
     if ((rc = launch_check("k_legal")) != 0) return rc;
     if (offsets) {
@@ -416,7 +473,9 @@ int jq_legal(jq_env *e, const int8_t *acting, int32_t *counts, int32_t *offsets,
         if ((rc = launch_check("k_scan")) != 0) return rc;
     }
     if (values) {
-        hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values);
+        if ((rc = csr_fits(e, offsets, values_capacity, strm(stream))) != 0) return rc;
+        hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values,
+                           values_capacity);
         if ((rc = launch_check("k_emit")) != 0) return rc;
     }
     return JQ_OK;
@@ -508,31 +567,48 @@ int jq_obs_decode_table(float *out)
     return JQ_OK;
 }
 
-int jq_sample_uniform(jq_env *e, const int32_t *counts, const int32_t *offsets, const int32_t *values, uint64_t seed,
-                      uint64_t ply, int32_t *out, void *stream)
+int jq_sample_uniform(jq_env *e, const int32_t *counts, const int32_t *offsets, const int32_t *values,
+                      int64_t values_capacity, uint64_t seed, uint64_t ply, int32_t *out, void *stream)
 {
     int rc = check_env(e);
     if (rc) return rc;
     if (!counts || !offsets || !values || !out) return fail(JQ_E_ARG, "null sampler buffer");
+    if (values_capacity < 0) return fail(JQ_E_ARG, "negative values capacity");
     hipLaunchKernelGGL(k_sample, dim3((e->S.n + 255) / 256), dim3(256), 0, strm(stream), e->S.n, counts, offsets,
-                       values, seed, ply, out);
+                       values, values_capacity, seed, ply, out);
     return launch_check("k_sample");
 }
 
-int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_t ply, int64_t reset_seed,
-                int32_t *counts, int32_t *offsets, int32_t *values, int32_t *mask_words, int32_t obs_fmt,
-                void *spatial, float *aux, float *global, uint8_t *terminated, float *reward, int32_t *actions_out,
-                void *stream)
+int jq_sample_logits(jq_env *e, const int8_t *acting, const int32_t *counts, const int32_t *offsets,
+                     const int32_t *values, int64_t values_capacity, uint64_t seed, uint64_t ply, int32_t *out,
+                     int32_t *canonical_out, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!counts || !offsets || !values || !out) return fail(JQ_E_ARG, "null sampler buffer");
+    if (values_capacity < 0) return fail(JQ_E_ARG, "negative values capacity");
+    hipLaunchKernelGGL(k_sample_logits, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, acting, counts, offsets,
+                       values, values_capacity, seed, ply, out, canonical_out);
+    return launch_check("k_sample_logits");
+}
+
+int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sample_seed, uint64_t ply,
+                int64_t reset_seed, int32_t *counts, int32_t *offsets, int32_t *values, int64_t values_capacity,
+                int32_t *mask_words, int32_t obs_fmt, void *spatial, float *aux, float *global, uint8_t *terminated,
+                float *reward, uint64_t *hash, int32_t *actions_out, void *stream)
 {
     int rc = check_env(e);
     if (rc) return rc;
     if (!counts || !offsets || !values) return fail(JQ_E_ARG, "env_step needs counts, offsets and values");
+    if (values_capacity < 0) return fail(JQ_E_ARG, "negative values capacity");
+    if (sampler != JQ_SAMPLE_UNIFORM && sampler != JQ_SAMPLE_LOGITS) return fail(JQ_E_ARG, "bad sampler %d", sampler);
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before stepping");
     if (spatial && (obs_fmt < JQ_OBS_F32 || obs_fmt > JQ_OBS_U8))
         return fail(JQ_E_ARG, "bad observation format %d", obs_fmt);
     EnvStepArgs A = {};
-    A.actions = actions; A.sample_seed = sample_seed; A.ply = ply; A.offsets = offsets; A.values = values;
-    A.actions_out = actions_out; A.O.term = terminated; A.O.reward = reward;
+    A.actions = actions; A.sampler = sampler; A.sample_seed = sample_seed; A.ply = ply; A.offsets = offsets;
+    A.values = values; A.values_cap = values_capacity;
+    A.actions_out = actions_out; A.O.term = terminated; A.O.reward = reward; A.O.hash = hash;
     A.do_reset = e->S.pool ? 1 : 0; A.reset_seed = reset_seed; A.counts = counts; A.mask_words = mask_words;
     // sample (unless actions are given), ply, restart from the pool and the
     // next seat's legal sets in one kernel
@@ -540,7 +616,9 @@ int jq_env_step(jq_env *e, const int32_t *actions, uint64_t sample_seed, uint64_
     if ((rc = launch_check("k_env_step")) != 0) return rc;
     hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, strm(stream), counts, offsets, e->S.n);
     if ((rc = launch_check("k_scan")) != 0) return rc;
-    hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values);
+    if ((rc = csr_fits(e, offsets, values_capacity, strm(stream))) != 0) return rc;
+    hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values,
+                       values_capacity);
     if ((rc = launch_check("k_emit")) != 0) return rc;
     // sequential on purpose: the u8 observation grid holds every CU's LDS, so a
     // concurrent launch only slows both down
@@ -609,7 +687,19 @@ int jq_finalize_import(jq_env *e, void *stream)
     int rc = check_env(e);
     if (rc) return rc;
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables first");
-    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 1);
+    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 1, nullptr);
+    if ((rc = launch_check("k_finalize")) != 0) return rc;
+    HIP_TRY(hipStreamSynchronize(strm(stream)));
+    return JQ_OK;
+}
+
+int jq_finalize_import_masked(jq_env *e, const uint8_t *env_mask, void *stream)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!env_mask) return fail(JQ_E_ARG, "null env mask");
+    if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables first");
+    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 1, env_mask);
     if ((rc = launch_check("k_finalize")) != 0) return rc;
     HIP_TRY(hipStreamSynchronize(strm(stream)));
     return JQ_OK;
@@ -620,7 +710,7 @@ int jq_rehash(jq_env *e, void *stream)
     int rc = check_env(e);
     if (rc) return rc;
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables first");
-    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 0);
+    hipLaunchKernelGGL(k_finalize, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, 0, nullptr);
     return launch_check("k_finalize");
 }
 
@@ -732,7 +822,7 @@ int jq_history_reconstruct(jq_history *h, const int64_t *flat, const int8_t *obs
         if ((rc = jq_observe(R, observer, fmt, 0, spatial, aux, global, stream)) != 0) return rc;
     }
     if (mask_words || mask_bool)
-        if ((rc = jq_legal(R, observer, nullptr, nullptr, nullptr, mask_words, mask_bool, stream)) != 0) return rc;
+        if ((rc = jq_legal(R, observer, nullptr, nullptr, nullptr, 0, mask_words, mask_bool, stream)) != 0) return rc;
     return JQ_OK;
 }
 

@@ -363,4 +363,25 @@ void generate_pool(uint64_t seed, int pool_size, int8_t *out)
         for (int s = 0; s < 4; ++s) lineup(rng, out + (size_t)p * 120 + 30 * s);
 }
 
+int validate_lineup(const int8_t *lu)
+{   // setup.py:60-136 (validate_lineup): C1-C5 over one seat's 30 slots
+    static const int kCount[14] = {0, 0, 1, 3, 2, 1, 1, 2, 2, 2, 2, 3, 3, 3};   // rules.py:131-147
+    int cnt[14] = {}, v = 0, nflag = 0, flag_at = -1;
+    for (int i = 0; i < 30; ++i)
+        if (lu[i] < 0 || lu[i] > 13) return LV_TYPE;   // PieceType(int(p)) raises
+    for (int i = 0; i < 30; ++i) {
+        const int t = lu[i];
+        ++cnt[t];
+        if (camp_slot(i) && t != 0) v |= LV_C1;
+        if (t == 2) { ++nflag; flag_at = i; }
+        if (t == 3 && i < 20) v |= LV_C3;   // landmines only in the back two rows (20..29)
+        if (t == 4 && i < 5) v |= LV_C4;    // no bomb in the front row (0..4)
+    }
+    if (nflag != 1 || !stronghold_slot(flag_at)) v |= LV_C2;
+    if (cnt[0] != 5 || cnt[1] != 0) v |= LV_C5;
+    for (int t = 2; t <= 13; ++t)
+        if (cnt[t] != kCount[t]) v |= LV_C5;
+    return v;
+}
+
 }  // namespace jq

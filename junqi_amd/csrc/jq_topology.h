@@ -76,4 +76,10 @@ int canonical_style(char c);
 void generate_styled(int mode, uint64_t seed, int count, bool per_game_seed, const int8_t *styles, int nstyles,
                      int8_t *out);
 
+// validate_lineup (setup.py:60-136) of one seat's 30 slots: 0 when C1-C5 hold,
+// else the LV_* bits of every rule broken (LV_TYPE alone for a value that is not
+// a PieceType).
+enum { LV_TYPE = 1, LV_C1 = 2, LV_C2 = 4, LV_C3 = 8, LV_C4 = 16, LV_C5 = 32 };
+int validate_lineup(const int8_t *lineup30);
+
 }  // namespace jq

@@ -215,7 +215,7 @@ class GpuRollout:
         if self._mask_bool is None:
             self._mask_bool = torch.empty((self.num_envs, FLAT_ACTION_DIM), dtype=torch.bool, device=self.device)
         s = None if seats is None else seats.to(device=self.device, dtype=torch.int8).contiguous()
-        L.check(L.lib.jq_legal(b._h, None if s is None else s.data_ptr(), b.counts.data_ptr(), None, None, None,
+        L.check(L.lib.jq_legal(b._h, None if s is None else s.data_ptr(), b.counts.data_ptr(), None, None, 0, None,
                                self._mask_bool.data_ptr(), b.stream))
         return self._mask_bool
 

@@ -1446,27 +1446,42 @@ int32_t jqo_reset_pool_index(int env, int64_t seed, int pool_size)
     return (int32_t)(h % (uint64_t)pool_size);
 }
 
+/* Digest of a legal-id row: sum of ids[j] * P^j mod 2^64, P = 0x100000001B3. */
+static uint64_t row_digest(const int32_t *ids, int m)
+{
+    uint64_t d = 0, w = 1;
+    for (int j = 0; j < m; j++) { d += (uint64_t)(uint32_t)ids[j] * w; w *= 0x100000001B3ull; }
+    return d;
+}
+
 /* `steps` rollout env-steps of n games (OpenMP over games): at env-step k each
- * game draws its action from the acting seat's legal ids with `sampler` (0
- * uniform, 1 masked logits) under (seed, ply0 + k), applies it, records the
- * acting team's reward (+-1 on the ply that ends the game), the terminated
- * flag and the Zobrist hash after the ply, then a finished game restarts from
- * pool[jqo_reset_pool_index(i, reset_seed0 + k)]. Outputs are (steps, n)
- * row-major; any may be NULL. Returns the number of plies applied. */
+ * game with k >= active_from[i] (all games when active_from is NULL) draws its
+ * action from the acting seat's legal ids with `sampler` (0 uniform, 1 masked
+ * logits) under (seed, ply0 + k) and applies it; the others take no action.
+ * Every game then records the acting team's reward (+-1 on the ply that ends
+ * the game), the terminated flag and the Zobrist hash after the ply; a
+ * finished game restarts from pool[jqo_reset_pool_index(i, reset_seed0 + k)];
+ * and the legal ids of the new acting seat are counted and digested
+ * (row_digest). Outputs are (steps, n) row-major; any may be NULL. Returns the
+ * number of plies applied. */
 long jqo_batch_rollout(jqo_game *gs, int n, const int8_t *pool, int pool_size, int sampler, uint64_t seed,
-                       uint64_t ply0, int64_t reset_seed0, int steps, float *reward, uint8_t *done,
-                       uint64_t *hash, int32_t *actions)
+                       uint64_t ply0, int64_t reset_seed0, int steps, const int32_t *active_from, float *reward,
+                       uint8_t *done, uint64_t *hash, int32_t *actions, int32_t *legal_count,
+                       uint64_t *legal_digest)
 {
     long applied = 0;
 #pragma omp parallel for schedule(dynamic, 16) reduction(+:applied)
     for (int i = 0; i < n; i++) {
         jqo_game *g = &gs[i];
         int32_t ids[4096];
+        int m = jqo_legal_ids(g, g->turn, ids, 4096);
         for (int k = 0; k < steps; k++) {
             size_t o = (size_t)k * n + i;
-            int seat = g->turn, m = jqo_legal_ids(g, seat, ids, 4096);
-            int32_t a = sampler ? jqo_sample_logits(ids, m, seat, i, seed, ply0 + k, NULL)
-                                : jqo_sample_uniform(ids, m, i, seed, ply0 + k);
+            int seat = g->turn;
+            int32_t a = -1;
+            if (!active_from || k >= active_from[i])
+                a = sampler ? jqo_sample_logits(ids, m, seat, i, seed, ply0 + k, NULL)
+                            : jqo_sample_uniform(ids, m, i, seed, ply0 + k);
             jqo_result r;
             memset(&r, 0, sizeof r);
             int rc = a >= 0 ? jqo_step(g, a / NC, a % NC, &r) : -1;
@@ -1480,7 +1495,19 @@ long jqo_batch_rollout(jqo_game *gs, int n, const int8_t *pool, int pool_size, i
                 int p = jqo_reset_pool_index(i, reset_seed0 + k, pool_size);
                 jqo_new_game(g, pool + (size_t)p * 120, g->show_mode, g->max_num_moves);
             }
+            m = jqo_legal_ids(g, g->turn, ids, 4096);
+            if (legal_count) legal_count[o] = m;
+            if (legal_digest) legal_digest[o] = row_digest(ids, m);
         }
     }
     return applied;
+}
+
+/* Observations of the acting seat of games [g0, g1) (OpenMP), rows from 0. */
+void jqo_batch_observe(const jqo_game *gs, int g0, int g1, float *spatial, float *glob)
+{
+#pragma omp parallel for schedule(dynamic, 8)
+    for (int i = g0; i < g1; i++)
+        jqo_observe(&gs[i], gs[i].turn, spatial + (size_t)(i - g0) * JQO_OBS_C * NC,
+                    glob + (size_t)(i - g0) * JQO_OBS_G);
 }

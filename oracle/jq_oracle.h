@@ -168,12 +168,16 @@ void jqo_batch_new(jqo_game *gs, int n, const int8_t *setups, int show_mode, int
 long jqo_batch_env_step(jqo_game *gs, int n, const int32_t *actions, int32_t *legal_counts,
                         uint8_t *mask_bits, float *obs_spatial, float *obs_global, int write_obs);
 
-/* Rollout: `steps` env-steps of sample (0 uniform, 1 masked logits) -> step ->
- * record reward / done / hash -> restart finished games from the pool.
+/* Rollout: `steps` env-steps of sample (0 uniform, 1 masked logits; games with
+ * k < active_from[i] take no action) -> step -> record reward / done / hash ->
+ * restart finished games from the pool -> count and digest the new legal row.
  * Outputs (steps, n) row-major, any may be NULL. */
 long jqo_batch_rollout(jqo_game *gs, int n, const int8_t *pool, int pool_size, int sampler, uint64_t seed,
-                       uint64_t ply0, int64_t reset_seed0, int steps, float *reward, uint8_t *done,
-                       uint64_t *hash, int32_t *actions);
+                       uint64_t ply0, int64_t reset_seed0, int steps, const int32_t *active_from, float *reward,
+                       uint8_t *done, uint64_t *hash, int32_t *actions, int32_t *legal_count,
+                       uint64_t *legal_digest);
+/* Acting-seat observations of games [g0, g1), rows from 0 (OpenMP). */
+void jqo_batch_observe(const jqo_game *gs, int g0, int g1, float *spatial, float *glob);
 
 #ifdef __cplusplus
 }

@@ -116,8 +116,9 @@ def lib() -> C.CDLL:
     L.jqo_sample_logits.argtypes = [P, I, I, I, C.c_uint64, C.c_uint64, P]
     L.jqo_sample_logits.restype = C.c_int32
     L.jqo_reset_pool_index.argtypes = [I, C.c_int64, I]; L.jqo_reset_pool_index.restype = C.c_int32
-    L.jqo_batch_rollout.argtypes = [P, I, P, I, I, C.c_uint64, C.c_uint64, C.c_int64, I, P, P, P, P]
+    L.jqo_batch_rollout.argtypes = [P, I, P, I, I, C.c_uint64, C.c_uint64, C.c_int64, I, P, P, P, P, P, P, P]
     L.jqo_batch_rollout.restype = C.c_long
+    L.jqo_batch_observe.argtypes = [P, I, I, P, P]
     L.jqo_init()
     assert L.jqo_sizeof_game() == GAME_DTYPE.itemsize, (L.jqo_sizeof_game(), GAME_DTYPE.itemsize)
     if RECENCY_LUT_PATH.exists():
@@ -391,18 +392,42 @@ class Batch:
                                             mb, sp, gl, 1 if obs else 0))
 
 
+LEGAL_DIGEST_P = 0x100000001B3
+
+
+def legal_digest(ids) -> int:
+    """Digest of one legal-id row as the rollout records it: sum ids[j] * P^j mod 2^64."""
+    d, w = 0, 1
+    for a in np.asarray(ids).tolist():
+        d = (d + (a & 0xFFFFFFFF) * w) & (2**64 - 1)
+        w = (w * LEGAL_DIGEST_P) & (2**64 - 1)
+    return d
+
+
 def rollout(batch: "Batch", pool: np.ndarray, *, sampler: int, seed: int, ply0: int, reset_seed0: int,
-            steps: int) -> dict:
-    """jqo_batch_rollout over a Batch: (steps, n) reward / done / hash / actions."""
+            steps: int, active_from: np.ndarray | None = None) -> dict:
+    """jqo_batch_rollout over a Batch: (steps, n) reward / done / hash / actions /
+    legal_count / legal_digest."""
     n = batch.n
     pool = np.ascontiguousarray(pool, dtype=np.int8).reshape(-1, 120)
     out = {"reward": np.zeros((steps, n), np.float32), "done": np.zeros((steps, n), np.uint8),
-           "hash": np.zeros((steps, n), np.uint64), "actions": np.zeros((steps, n), np.int32)}
+           "hash": np.zeros((steps, n), np.uint64), "actions": np.zeros((steps, n), np.int32),
+           "legal_count": np.zeros((steps, n), np.int32), "legal_digest": np.zeros((steps, n), np.uint64)}
+    au = None if active_from is None else np.ascontiguousarray(active_from, dtype=np.int32)
     applied = lib().jqo_batch_rollout(_p(batch.games), n, _p(pool), len(pool), sampler, seed, ply0, reset_seed0,
-                                      steps, _p(out["reward"]), _p(out["done"]), _p(out["hash"]),
-                                      _p(out["actions"]))
+                                      steps, None if au is None else _p(au), _p(out["reward"]), _p(out["done"]),
+                                      _p(out["hash"]), _p(out["actions"]), _p(out["legal_count"]),
+                                      _p(out["legal_digest"]))
     out["applied"] = int(applied)
     return out
+
+
+def batch_observe(batch: "Batch", g0: int, g1: int) -> tuple[np.ndarray, np.ndarray]:
+    """Acting-seat float32 observations of games [g0, g1)."""
+    sp = np.zeros((g1 - g0, OBS_C, 17, 17), np.float32)
+    gl = np.zeros((g1 - g0, OBS_G), np.float32)
+    lib().jqo_batch_observe(_p(batch.games), g0, g1, _p(sp), _p(gl))
+    return sp, gl
 
 
 def omp_threads() -> int:

@@ -128,25 +128,13 @@ def canonical_mask_words(ids: np.ndarray, seat: int, tables: dict) -> np.ndarray
 
 
 def reset_pool_index(env: int, seed: int, pool_size: int) -> int:
-    """Pool pick of the device auto-reset (reference game_state.cu:2986-2991)."""
-    m = (1 << 64) - 1
-    h = (env * 2654435761 + (seed & m)) & m
-    h ^= h >> 17
-    h = (h * 0xbf58476d1ce4e5b9) & m
-    h ^= h >> 31
-    return h % pool_size
+    """Pool pick of the device auto-reset (reference game_state.cu:2997-3001), from the oracle."""
+    return O.reset_pool_index(env, seed, pool_size)
 
 
 def philox_first_word(c0: int, c1: int, c2: int, c3: int, k0: int, k1: int) -> int:
-    """Philox4x32-10 (Salmon et al., SC'11), first output word."""
-    M = 0xFFFFFFFF
-    for _ in range(10):
-        p0 = 0xD2511F53 * c0
-        p1 = 0xCD9E8D57 * c2
-        c0, c1, c2, c3 = ((p1 >> 32) ^ c1 ^ k0) & M, p1 & M, ((p0 >> 32) ^ c3 ^ k1) & M, p0 & M
-        k0 = (k0 + 0x9E3779B9) & M
-        k1 = (k1 + 0xBB67AE85) & M
-    return c0
+    """Philox4x32-10 first output word, from the oracle (pinned by the Random123 vectors)."""
+    return O.philox4x32_10((c0, c1, c2, c3), (k0, k1))[0]
 
 
 def philox_first_word_np(c0: np.ndarray, c1: int, c2: int, c3: int, k0: int, k1: int) -> np.ndarray:
@@ -162,6 +150,35 @@ def philox_first_word_np(c0: np.ndarray, c1: int, c2: int, c3: int, k0: int, k1:
         k0 = (k0 + np.uint64(0x9E3779B9)) & M
         k1 = (k1 + np.uint64(0xBB67AE85)) & M
     return c0
+
+
+def oracle_pack(games: list) -> dict[str, np.ndarray]:
+    """The oracle games as the flat dict of DeviceGameStateBatch.copy_to_host /
+    _pack_from_batched (bindings.cpp:117-183, junqi_rl/gpu_rollout.py:447-483)."""
+    g = np.concatenate([gm.buf for gm in games])
+    alive = g["alive"].astype(bool)
+    flat = lambda a: np.ascontiguousarray(a).reshape(-1)  # noqa: E731
+    return {
+        "cell_piece_id_per_piece": flat(np.where(alive, flat_pos(g["pos_x"], g["pos_y"]), -1).astype(np.int16)),
+        "piece_seat_arr": flat(g["pseat"].astype(np.int8)),
+        "piece_type_arr": flat(g["ptype"].astype(np.int8)),
+        "alive": flat(alive),
+        "pos_x": flat(g["pos_x"].astype(np.int8)), "pos_y": flat(g["pos_y"].astype(np.int8)),
+        "zero_x": flat(g["zero_x"].astype(np.int8)), "zero_y": flat(g["zero_y"].astype(np.int8)),
+        "move_count_arr": flat(g["move_count"].astype(np.int16)),
+        "active_eat_arr": flat(g["active_eat"].astype(np.int16)),
+        "passive_surv_arr": flat(g["passive_surv"].astype(np.int16)),
+        "death_reason_arr": flat(g["death_reason"].astype(np.int8)),
+        "death_step_arr": flat(g["death_step"].astype(np.int16)),
+        "death_loc_flat_arr": flat(g["death_loc"].astype(np.int16)),
+        "cell_piece_id": flat(g["cell_pid"].astype(np.int16)),
+        "seat_dead_arr": flat(g["seat_dead"].astype(bool)),
+        "seat_flag_revealed_arr": flat(g["flag_rev"].astype(bool)),
+        "turn": flat(g["turn"].astype(np.int8)),
+        "zobrist": flat(g["zobrist"].view(np.int64)),
+        "move_counter": flat(g["move_counter"].astype(np.int32)),
+        "moves_since_last_combat": flat(g["mslc"].astype(np.int32)),
+    }
 
 
 def oracle_games_from_lineups(lineups: np.ndarray, show_mode: int, max_num_moves: int = 4000) -> list:

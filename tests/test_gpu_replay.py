@@ -58,7 +58,8 @@ def test_recorded_games_round_trip_through_jql(jq):
         out = b.legal()
         acts = torch.empty(n, dtype=torch.int32, device=b.device)
         jq._lib.check(jq._lib.lib.jq_sample_uniform(b._h, out["counts"].data_ptr(), out["offsets"].data_ptr(),
-                                                    out["values"].data_ptr(), 9, ply, acts.data_ptr(), b.stream))
+                                                    out["values"].data_ptr(), out["values"].numel(), 9, ply,
+                                                    acts.data_ptr(), b.stream))
         rec.record(b.step(acts))
     zob = b.get_field("zobrist")[:, 0]
     for i in range(n):

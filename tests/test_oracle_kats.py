@@ -710,3 +710,16 @@ def test_reset_pool_index_closed_form():
         h = (h * 0xBF58476D1CE4E5B9) & (2**64 - 1)
         h ^= h >> 31
         assert O.reset_pool_index(env, seed, size) == h % size
+
+
+def test_vectorised_philox_helper_equals_oracle():
+    """tests/gpu_compare.philox_first_word_np (used over 32,768 envs at once by the
+    full-size GPU tests) equals the pinned oracle generator."""
+    from tests import gpu_compare as G
+
+    rng = np.random.default_rng(5)
+    c0 = rng.integers(0, 2**32, 200, dtype=np.uint64)
+    for c1, c2, c3, k0, k1 in ((3, 0, 0, 0x4A51, 0), (2**32 - 1, 7, 9, 1, 2**32 - 1)):
+        got = G.philox_first_word_np(c0, c1, c2, c3, k0, k1)
+        want = [O.philox4x32_10((int(a), c1, c2, c3), (k0, k1))[0] for a in c0]
+        assert got.tolist() == want
