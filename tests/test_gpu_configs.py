@@ -40,14 +40,12 @@ def jq():
     return junqi_amd
 
 
-_P = np.uint64(O.LEGAL_DIGEST_P)
-
-
 def _pow_table(m: int) -> torch.Tensor:
-    w = np.ones(m, np.uint64)
-    for j in range(1, m):
-        w[j] = w[j - 1] * _P
-    return torch.from_numpy(w.view(np.int64))
+    w, x = [], 1
+    for _ in range(m):
+        w.append(x)
+        x = (x * O.LEGAL_DIGEST_P) & (2**64 - 1)
+    return torch.from_numpy(np.array(w, np.uint64).view(np.int64))
 
 
 def _row_digests(b, pw: torch.Tensor) -> torch.Tensor:
@@ -171,7 +169,7 @@ def test_c3_mixed_stage_observations_16384(jq, show_mode):
             assert np.array_equal(got, osp), f"c3 u8 observation, games {g0}-{g1}, ply {k}"
             assert np.array_equal(gl8[g0:g1].cpu().numpy(), ogl)
             if sp16 is not None:
-                assert np.array_equal(sp16[g0:g1].cpu().numpy().view(np.uint16), _bf16_rne(osp)), \
+                assert np.array_equal(sp16[g0:g1].view(torch.int16).cpu().numpy().view(np.uint16), _bf16_rne(osp)), \
                     f"c3 bf16 observation, games {g0}-{g1}"
                 assert np.array_equal(gl16[g0:g1].cpu().numpy(), ogl)
     b.close()
