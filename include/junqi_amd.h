@@ -325,6 +325,19 @@ int jq_history_reconstruct(jq_history *hist, const int64_t *flat, const int8_t *
                            void *spatial, float *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
                            void *stream);
 
+/* The same rebuild with no device allocation: for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The rebuilt rows live in one
+ * file-scope device array of the library, JQ_NOALLOC_MAX_ROWS rows (21.45 MB,
+ * held on each device the library runs on until the process ends), shared by
+ * every call on that device: calls that overlap on one device race, so keep
+ * them on one stream or serialise them. batch > JQ_NOALLOC_MAX_ROWS returns
+ * JQ_E_ARG; split larger minibatches. Outputs equal jq_history_reconstruct's. */
+#define JQ_NOALLOC_MAX_ROWS 1024
+int jq_history_reconstruct_noalloc(jq_history *hist, const int64_t *flat, const int8_t *observer, int32_t batch,
+                                   int32_t fmt, void *spatial, float *aux, float *global, int32_t *mask_words,
+                                   uint8_t *mask_bool, void *stream);
+
 /* ---- legal-support storage: dense mask rows <-> id lists ----------------------
  * Rollout buffers keep each transition's legal support as ids
  * (junqi_rl/training/rollout_gpu.py:119-198). jq_mask_count: counts (device

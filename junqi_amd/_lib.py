@@ -27,6 +27,7 @@ AUX_PLANES = 6
 MAX_LEGAL = 3200
 SLOTS_PER_PIECE = 80
 SETUP_CANONICAL, SETUP_MIXED = 1, 2
+NOALLOC_MAX_ROWS = 1024
 AUX_CHANNELS = (64, 65, 253, 254, 255, 256)
 
 FIELDS = {
@@ -47,7 +48,7 @@ _EXPORTS = [
     "jq_env_step", "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import",
     "jq_finalize_import_masked", "jq_rehash", "jq_validate_lineup",
     "jq_sync", "jq_history_create", "jq_history_destroy", "jq_history_bytes", "jq_history_snapshot",
-    "jq_history_reconstruct", "jq_mask_count", "jq_mask_to_ids", "jq_ids_to_mask", "jq_upload_beliefs",
+    "jq_history_reconstruct", "jq_history_reconstruct_noalloc", "jq_mask_count", "jq_mask_to_ids", "jq_ids_to_mask", "jq_upload_beliefs",
     "jq_clear_beliefs",
 ]
 
@@ -105,6 +106,7 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_history_destroy": ([P], C.c_int), "jq_history_bytes": ([P, C.POINTER(I64)], C.c_int),
         "jq_history_snapshot": ([P, P, P, I32, P], C.c_int),
         "jq_history_reconstruct": ([P, P, P, I32, I32, P, P, P, P, P, P], C.c_int),
+        "jq_history_reconstruct_noalloc": ([P, P, P, I32, I32, P, P, P, P, P, P], C.c_int),
         "jq_mask_count": ([P, I32, I32, P, P], C.c_int), "jq_mask_to_ids": ([P, I32, I32, I32, P, P], C.c_int),
         "jq_ids_to_mask": ([P, P, I64, I32, P, I32, I32, P, P], C.c_int),
         "jq_upload_beliefs": ([P, P, I32, P], C.c_int), "jq_clear_beliefs": ([P], C.c_int),

@@ -38,7 +38,9 @@ __device__ __forceinline__ void copy_words(T *__restrict__ dst, const T *__restr
 
 // Row i of R <- history row flat[i]; rows outside [0, steps * n) become the
 // empty terminated state. One 256-thread block per row, 16-byte copies where
-// the blocks allow (the 292-byte board moves in 4-byte words).
+// the blocks allow (the 292-byte board moves in 4-byte words). A state with no
+// full combat-memory records (R.cm null) gets only the summaries, views and
+// eaten-by sets that observations and legal masks read.
 __global__ __launch_bounds__(256) void k_history_gather(HistState H, const int64_t *__restrict__ flat, int batch, State R)
 {
     const int i = blockIdx.x, t = threadIdx.x;
@@ -52,9 +54,10 @@ __global__ __launch_bounds__(256) void k_history_gather(HistState H, const int64
                reinterpret_cast<const uint32_t *>(H.cell + (size_t)f * CELL_STRIDE), CELL_STRIDE / 4, t, 256);
     copy_words(reinterpret_cast<uint4 *>(R.piece + (size_t)i * PID_STRIDE),
                reinterpret_cast<const uint4 *>(H.piece + (size_t)f * PID_STRIDE), PID_STRIDE, t, 256);
-    copy_words(reinterpret_cast<uint4 *>(R.cm + (size_t)i * 4 * PID_STRIDE),
-               reinterpret_cast<const uint4 *>(H.cm + (size_t)f * 4 * PID_STRIDE),
-               4 * PID_STRIDE * (int)(sizeof(CmRec) / 16), t, 256);
+    if (R.cm)
+        copy_words(reinterpret_cast<uint4 *>(R.cm + (size_t)i * 4 * PID_STRIDE),
+                   reinterpret_cast<const uint4 *>(H.cm + (size_t)f * 4 * PID_STRIDE),
+                   4 * PID_STRIDE * (int)(sizeof(CmRec) / 16), t, 256);
     copy_words(reinterpret_cast<uint4 *>(R.cme + (size_t)i * 4 * PID_STRIDE),
                reinterpret_cast<const uint4 *>(H.cme + (size_t)f * 4 * PID_STRIDE), 4 * PID_STRIDE, t, 256);
     for (int k = t; k < 4 * PID_STRIDE; k += 256) {   // summaries and views are not stored: derive them

@@ -840,7 +840,7 @@ __device__ __forceinline__ void clear_env(const State &S, int env, int t, int nt
     for (int p = t; p < PID_STRIDE; p += nt) {
         S.piece[pc_idx(env, p)] = r;
         for (int o = 0; o < 4; ++o) {
-            S.cm[cm_idx(env, o, p)] = c;
+            if (S.cm) S.cm[cm_idx(env, o, p)] = c;   // a rebuild-only state keeps no full records
             S.cme[cm_idx(env, o, p)] = ce;
             S.cmk[cm_idx(env, o, p)] = 0;
             S.cmv[cm_idx(env, o, p)] = cv;

@@ -826,6 +826,106 @@ int jq_history_reconstruct(jq_history *h, const int64_t *flat, const int8_t *obs
     return JQ_OK;
 }
 
+// ------------------------------------------------ history rebuild without allocation
+// Rebuild-only state for jq_history_reconstruct_noalloc: the arrays the gather,
+// the observation and the legal masks touch, for at most JQ_NOALLOC_MAX_ROWS
+// rows, carved from one file-scope device array (no full combat-memory
+// records: the rebuild reads only their summaries, views and eaten-by sets).
+// 20,948 bytes per row, 21.45 MB in all on each device the library runs on.
+namespace {
+constexpr size_t NA_ROWS = JQ_NOALLOC_MAX_ROWS;
+constexpr size_t na_up(size_t x) { return (x + 255) & ~size_t(255); }
+constexpr size_t NA_CELL = 0;
+constexpr size_t NA_PIECE = NA_CELL + na_up(NA_ROWS * CELL_STRIDE);
+constexpr size_t NA_CME = NA_PIECE + na_up(NA_ROWS * PID_STRIDE * sizeof(PieceRec));
+constexpr size_t NA_CMK = NA_CME + na_up(NA_ROWS * 4 * PID_STRIDE * sizeof(CmEat));
+constexpr size_t NA_CMV = NA_CMK + na_up(NA_ROWS * 4 * PID_STRIDE);
+constexpr size_t NA_BCODE = NA_CMV + na_up(NA_ROWS * 4 * PID_STRIDE * sizeof(CmView));
+constexpr size_t NA_REM = NA_BCODE + na_up(NA_ROWS * 4 * PID_STRIDE);
+constexpr size_t NA_ENV = NA_REM + na_up(NA_ROWS * 4 * 48);
+constexpr size_t NA_HIST = NA_ENV + na_up(NA_ROWS * sizeof(EnvRec));
+constexpr size_t NA_LG = NA_HIST + na_up(NA_ROWS * HIST_LEN * sizeof(int32_t));
+constexpr size_t NA_BYTES = NA_LG + na_up(NA_ROWS * sizeof(LegalRec));
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[NA_BYTES];
+
+namespace {
+std::mutex g_na_mu;
+uint8_t *g_na_ptr[64] = {};    // device address of `scratch` on each device
+jq_env g_na_env[64];           // host view of each device's rebuild state
+
+// Per device, once: the device address of `scratch` (the array's name is a
+// host-side stand-in and must never reach a kernel) and the state over it.
+int noalloc_state(int device, jq_env *&out)
+{
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    if (device < 0 || device >= 64) return fail(JQ_E_ARG, "device %d out of range", device);
+    if (!g_na_ptr[device]) {
+        int rc = ensure_device_tables(device);
+        if (rc) return rc;
+        void *p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p)
+            return fail(JQ_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(err));
+        uint8_t *b = static_cast<uint8_t *>(p);
+        jq_env &e = g_na_env[device];
+        e.device = device;
+        State &S = e.S;
+        S.cell = reinterpret_cast<int8_t *>(b + NA_CELL);
+        S.piece = reinterpret_cast<PieceRec *>(b + NA_PIECE);
+        S.cm = nullptr;
+        S.cme = reinterpret_cast<CmEat *>(b + NA_CME);
+        S.cmk = b + NA_CMK;
+        S.cmv = reinterpret_cast<CmView *>(b + NA_CMV);
+        S.bcode = b + NA_BCODE;
+        S.rem = reinterpret_cast<int8_t *>(b + NA_REM);
+        S.env = reinterpret_cast<EnvRec *>(b + NA_ENV);
+        S.hist = reinterpret_cast<int32_t *>(b + NA_HIST);
+        S.lg = reinterpret_cast<LegalRec *>(b + NA_LG);
+        S.ztab = nullptr;
+        S.pool = nullptr;
+        S.pool_size = 0;
+        g_na_ptr[device] = b;
+    }
+    out = &g_na_env[device];
+    return JQ_OK;
+}
+}  // namespace
+
+extern "C" int jq_history_reconstruct_noalloc(jq_history *h, const int64_t *flat, const int8_t *observer,
+                                              int32_t batch, int32_t fmt, void *spatial, float *aux, float *global,
+                                              int32_t *mask_words, uint8_t *mask_bool, void *stream)
+{
+    if (!h) return fail(JQ_E_ARG, "null history");
+    if (batch <= 0) return fail(JQ_E_ARG, "cannot reconstruct an empty history minibatch");
+    if (batch > JQ_NOALLOC_MAX_ROWS)
+        return fail(JQ_E_ARG, "batch %d exceeds the %d rows jq_history_reconstruct_noalloc holds", batch,
+                    JQ_NOALLOC_MAX_ROWS);
+    if (!flat || !observer) return fail(JQ_E_ARG, "history reconstruction received a null device pointer");
+    if (!h->rlut_ready) return fail(JQ_E_STATE, "history has no snapshot yet");
+    HIP_TRY(hipSetDevice(h->device));
+    jq_env *R = nullptr;
+    int rc = noalloc_state(h->device, R);
+    if (rc) return rc;
+    R->S.n = batch;
+    R->S.max_moves = std::max(1, h->max_moves);
+    R->S.show_mode = h->show_mode;
+    R->S.rlut = h->rlut;
+    R->rlut_ready = true;
+    R->zob_ready = false;
+    R->ext_on = false;
+    hipLaunchKernelGGL(k_history_gather, dim3(batch), dim3(256), 0, strm(stream), h->H, flat, batch, R->S);
+    if ((rc = launch_check("k_history_gather")) != 0) return rc;
+    if (spatial || aux || global) {
+        if (!spatial || !global) return fail(JQ_E_ARG, "spatial and global outputs go together");
+        if ((rc = jq_observe(R, observer, fmt, 0, spatial, aux, global, stream)) != 0) return rc;
+    }
+    if (mask_words || mask_bool)
+        if ((rc = jq_legal(R, observer, nullptr, nullptr, nullptr, 0, mask_words, mask_bool, stream)) != 0) return rc;
+    return JQ_OK;
+}
+
 // ---------------------------------------------------------------- masks
 int jq_mask_count(const uint8_t *mask, int32_t n, int32_t d, int32_t *counts, void *stream)
 {
