@@ -3,7 +3,7 @@
 One step = for every game: draw an action uniformly from its legal row
 (Philox4x32-10), apply the ply, auto-reset finished games from the setup pool,
 generate the next acting seat's legal actions (sorted CSR + packed canonical
-mask) and its 317-plane observation (u8 codes + f32 aux planes + 28 globals).
+mask) and its 317-plane observation (u8 codes + aux rows + 28 globals).
 Prints one JSON line. Usage: python bench.py [--steps K] [--warmup W] [--envs N]
 """
 
@@ -21,7 +21,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 OBS_U8_BYTES = 317 * 289          # 91,613
-AUX_BYTES = 6 * 289 * 4           # 6,936
+AUX_BYTES = 8 + 4 * 289 * 2       # 2,320: turn history f32[2] + recency codes u16[4][289]
 GLOBAL_BYTES = 28 * 4             # 112
 MASK_BYTES = 521 * 4              # 2,084
 
@@ -140,7 +140,7 @@ def main() -> int:
     es = {"u8": 1, "bf16": 2, "f32": 4}[args.fmt]
     sdt = {"u8": torch.uint8, "bf16": torch.bfloat16, "f32": torch.float32}[args.fmt]
     spatial = torch.empty((n, 317, 17, 17), dtype=sdt, device=dev)
-    aux = torch.empty((n, 6, 17, 17), dtype=torch.float32, device=dev) if args.fmt == "u8" else None
+    aux = torch.empty((n, AUX_BYTES), dtype=torch.uint8, device=dev) if args.fmt == "u8" else None
     glob = torch.empty((n, 28), dtype=torch.float32, device=dev)
     term = torch.empty(n, dtype=torch.uint8, device=dev)
     reward = torch.empty(n, dtype=torch.float32, device=dev)

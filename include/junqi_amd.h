@@ -26,7 +26,7 @@ extern "C" {
 #define JQ_OBS_GLOBALS 28
 #define JQ_ACTION_DIM 16641        /* 129 * 129 compact canonical actions */
 #define JQ_MASK_WORDS 521          /* 32-bit words per packed canonical mask row */
-#define JQ_AUX_PLANES 6            /* continuous planes carried in fp32 by the u8 format */
+#define JQ_AUX_BYTES 2320          /* u8 aux row: float32[2] turn history + uint16[4][289] recency codes */
 #define JQ_MAX_LEGAL 3200          /* per-env upper bound on legal actions (25 pieces x 128) */
 /* setup styles for jq_generate_styled */
 #define JQ_SETUP_CANONICAL 1
@@ -56,7 +56,7 @@ extern "C" {
 /* observation output formats */
 #define JQ_OBS_F32 0       /* (N,317,17,17) float32, the reference layout */
 #define JQ_OBS_BF16 1      /* (N,317,17,17) bfloat16 = round-to-nearest-even of the f32 */
-#define JQ_OBS_U8 2        /* (N,317,17,17) uint8 codes + (N,6,17,17) float32 aux planes */
+#define JQ_OBS_U8 2        /* (N,317,17,17) uint8 codes + (N,JQ_AUX_BYTES) aux rows, see jq_observe */
 
 /* action formats for jq_step */
 #define JQ_ACT_WORLD 0     /* src_flat*289 + dst_flat in the world frame */
@@ -176,14 +176,20 @@ int jq_legal_slots(jq_env *env, const int8_t *acting, uint8_t *slots, void *stre
 
 /* Observation of `observer` (device int8 N; NULL = current turn) in that seat's
  * canonical frame. fmt JQ_OBS_*; spatial: device (N,317,17,17) of the format's
- * element type; aux: device float (N,6,17,17) for JQ_OBS_U8 (else NULL);
- * global: device float (N,28). all_seats != 0 writes (N,4,...) rows; then
+ * element type; global: device float (N,28). JQ_OBS_U8 writes value codes
+ * (jq_obs_decode_table maps them to the float32 values) and leaves the six
+ * continuous planes zero; `aux` (device, 16-byte aligned, JQ_AUX_BYTES per row;
+ * NULL to skip; NULL for the other formats) carries them: bytes 0-7 the float32
+ * values of turn-history planes 64 and 65 (each constant over its plane), then
+ * uint16 codes [4][289] of recency planes 253-256 per canonical cell, 0 for 0.0
+ * and c > 0 for recency_table[plane - 253][c - 1] (jq_upload_recency's table,
+ * exp(-(c - 1) / tau)). all_seats != 0 writes (N,4,...) rows; then
  * `observer` is an optional device int8 (N,4) observer map (slot k of env i
  * observes seat observer[i*4+k]; NULL = seat k), as upload_observer_seats sets
  * it (junqi_rl/gpu_rollout.py:983-1001). Replaces build_observation_single_seat /
  * build_observation_batch_resident (observation.cu:648-802). */
 int jq_observe(jq_env *env, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial,
-               float *aux, float *global, void *stream);
+               void *aux, float *global, void *stream);
 
 /* Uploaded beliefs: copy (N, 4, 12, 289) float32 world-cell beliefs per (env,
  * observer) into the handle (from host memory if from_host, else from device
@@ -231,7 +237,7 @@ int jq_sample_logits(jq_env *env, const int8_t *acting, const int32_t *counts, c
  * action taken (world id, -1 none). */
 int jq_env_step(jq_env *env, const int32_t *actions, int32_t sampler, uint64_t sample_seed, uint64_t ply,
                 int64_t reset_seed, int32_t *counts, int32_t *offsets, int32_t *values, int64_t values_capacity,
-                int32_t *mask_words, int32_t obs_fmt, void *spatial, float *aux, float *global,
+                int32_t *mask_words, int32_t obs_fmt, void *spatial, void *aux, float *global,
                 uint8_t *terminated, float *reward, uint64_t *hash, int32_t *actions_out, void *stream);
 
 /* State import / export (host memory), one field at a time. Replaces
@@ -322,7 +328,7 @@ int jq_history_snapshot(jq_history *hist, jq_env *env, const int8_t *acting, int
  * scratch of `batch` rows is kept between calls (grown when needed), so calls
  * on one history must not overlap on different streams. */
 int jq_history_reconstruct(jq_history *hist, const int64_t *flat, const int8_t *observer, int32_t batch, int32_t fmt,
-                           void *spatial, float *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
+                           void *spatial, void *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
                            void *stream);
 
 /* The same rebuild with no device allocation: for callers that cannot allocate
@@ -335,7 +341,7 @@ int jq_history_reconstruct(jq_history *hist, const int64_t *flat, const int8_t *
  * JQ_E_ARG; split larger minibatches. Outputs equal jq_history_reconstruct's. */
 #define JQ_NOALLOC_MAX_ROWS 1024
 int jq_history_reconstruct_noalloc(jq_history *hist, const int64_t *flat, const int8_t *observer, int32_t batch,
-                                   int32_t fmt, void *spatial, float *aux, float *global, int32_t *mask_words,
+                                   int32_t fmt, void *spatial, void *aux, float *global, int32_t *mask_words,
                                    uint8_t *mask_bool, void *stream);
 
 /* ---- legal-support storage: dense mask rows <-> id lists ----------------------

@@ -8,10 +8,10 @@ built; there is no CPU implementation behind it.
 
 from . import _lib
 from ._lib import AUX_CHANNELS, SLOTS_PER_PIECE, JunqiError
-from .batch import JunqiBatch, decode_table, generate_lineups, generate_pool, recency_table, zobrist_stream
+from .batch import JunqiBatch, decode_table, decode_u8, generate_lineups, generate_pool, recency_table, zobrist_stream
 from .gpu_rollout import GpuRollout
 from .gpu_world import GpuWorld
 from .history import GpuRolloutHistory
 
-__all__ = ["JunqiBatch", "GpuRollout", "GpuWorld", "GpuRolloutHistory", "JunqiError", "AUX_CHANNELS", "SLOTS_PER_PIECE", "decode_table",
+__all__ = ["JunqiBatch", "GpuRollout", "GpuWorld", "GpuRolloutHistory", "JunqiError", "AUX_CHANNELS", "SLOTS_PER_PIECE", "decode_table", "decode_u8",
            "generate_lineups", "generate_pool", "recency_table", "zobrist_stream", "_lib"]

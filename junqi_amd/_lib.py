@@ -23,7 +23,7 @@ ACTION_DIM = 16641
 MASK_WORDS = 521
 OBS_CHANNELS = 317
 OBS_GLOBALS = 28
-AUX_PLANES = 6
+AUX_BYTES = 2320   # u8 aux row: float32[2] turn history + uint16[4][289] recency codes
 MAX_LEGAL = 3200
 SLOTS_PER_PIECE = 80
 SETUP_CANONICAL, SETUP_MIXED = 1, 2

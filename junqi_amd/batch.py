@@ -57,6 +57,42 @@ def decode_table() -> np.ndarray:
     return out
 
 
+def _split_aux(aux):
+    """(..., 2320) aux rows -> turn-history floats (..., 2) and recency codes (..., 4, 289)."""
+    if isinstance(aux, torch.Tensor):
+        turn = aux[..., :8].contiguous().view(torch.float32)
+        codes = aux[..., 8:].contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+        return turn, codes.reshape(aux.shape[:-1] + (4, 289))
+    a = np.ascontiguousarray(aux)
+    return a[..., :8].copy().view(np.float32), a[..., 8:].copy().view(np.uint16).astype(np.int64).reshape(
+        a.shape[:-1] + (4, 289))
+
+
+def decode_u8(spatial, aux):
+    """float32 observation (..., 317, 17, 17) from JQ_OBS_U8 codes and aux rows
+    (torch tensors on any device, or numpy arrays): codes through the decode
+    table, planes 64-65 from the aux floats, planes 253-256 from the recency
+    table at the aux codes."""
+    if isinstance(spatial, torch.Tensor):
+        dev = spatial.device
+        dec = torch.from_numpy(decode_table()).to(dev)
+        out = dec[spatial.long()]
+        turn, codes = _split_aux(aux)
+        out[..., 64:66, :, :] = turn[..., :, None, None]
+        rl = torch.from_numpy(recency_table().reshape(4, 4096)).to(dev)
+        q = torch.arange(4, device=dev).view((1,) * (codes.dim() - 2) + (4, 1)).expand_as(codes)
+        vals = torch.where(codes > 0, rl[q, (codes - 1).clamp(min=0)], torch.zeros((), device=dev))
+        out[..., 253:257, :, :] = vals.reshape(codes.shape[:-1] + (17, 17))
+        return out
+    out = decode_table()[np.asarray(spatial)]
+    turn, codes = _split_aux(aux)
+    out[..., 64:66, :, :] = turn[..., :, None, None]
+    rl = recency_table().reshape(4, 4096)
+    vals = np.where(codes > 0, rl[np.arange(4)[:, None], np.maximum(codes - 1, 0)], np.float32(0))
+    out[..., 253:257, :, :] = vals.reshape(codes.shape[:-1] + (17, 17)).astype(np.float32)
+    return out
+
+
 _CM_FIELDS = ("cm_direct_lo", "cm_direct_hi", "cm_direct_type", "cm_last_direct", "cm_other_count",
               "cm_chain_lo", "cm_chain_hi", "cm_chain_type", "cm_last_chain", "cm_eaten_lo", "cm_eaten_hi",
               "cm_floor", "cm_floor_step", "cm_flags")
@@ -227,7 +263,7 @@ class JunqiBatch:
         if out_global is None:
             out_global = torch.empty(lead + (L.OBS_GLOBALS,), dtype=torch.float32, device=self.device)
         if fmt == "u8" and out_aux is None:
-            out_aux = torch.empty(lead + (L.AUX_PLANES, 17, 17), dtype=torch.float32, device=self.device)
+            out_aux = torch.empty(lead + (L.AUX_BYTES,), dtype=torch.uint8, device=self.device)
         if tuple(out_spatial.shape) != lead + (L.OBS_CHANNELS, 17, 17) or out_spatial.dtype != dt:
             raise ValueError("out_spatial has the wrong shape or dtype")
         s = None if observer is None else observer.to(device=self.device, dtype=torch.int8).contiguous()

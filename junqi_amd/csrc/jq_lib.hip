@@ -493,7 +493,7 @@ int jq_legal_slots(jq_env *e, const int8_t *acting, uint8_t *slots, void *stream
     return launch_check("k_slots");
 }
 
-int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial, float *aux,
+int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats, void *spatial, void *aux,
                float *global, void *stream)
 {
     int rc = check_env(e);
@@ -501,8 +501,10 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
     if (!spatial) return fail(JQ_E_ARG, "null spatial output");
     if (fmt < JQ_OBS_F32 || fmt > JQ_OBS_U8) return fail(JQ_E_ARG, "bad observation format %d", fmt);
     const int es = fmt == JQ_OBS_F32 ? 4 : fmt == JQ_OBS_BF16 ? 2 : 1;
-    if ((uintptr_t)spatial % es || (aux && (uintptr_t)aux % 4) || (global && (uintptr_t)global % 4))
+    if ((uintptr_t)spatial % es || (global && (uintptr_t)global % 4))
         return fail(JQ_E_ARG, "observation buffers must be aligned to their element size");
+    if (aux && fmt != JQ_OBS_U8) return fail(JQ_E_ARG, "aux rows belong to the u8 format only");
+    if (aux && (uintptr_t)aux % 16) return fail(JQ_E_ARG, "u8 aux rows must be 16-byte aligned");
     if ((fmt != JQ_OBS_U8 || aux) && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
     const int nrows = all_seats ? e->S.n * 4 : e->S.n;
     const dim3 grid(nrows), block(OBS_THREADS);
@@ -525,8 +527,8 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
     default:
         if ((rc = obs_u8_grid(e)) != 0) return rc;
         hipLaunchKernelGGL(k_observe_u8_persist, dim3(std::min(nrows, e->obs_blocks)), dim3(OBS_THREADS), 0,
-                           strm(stream), e->S, observer, all_seats, static_cast<uint8_t *>(spatial), aux, global,
-                           nrows);
+                           strm(stream), e->S, observer, all_seats, static_cast<uint8_t *>(spatial),
+                           static_cast<uint8_t *>(aux), global, nrows);
         break;
     }
     return launch_check("k_observe");
@@ -594,7 +596,7 @@ int jq_sample_logits(jq_env *e, const int8_t *acting, const int32_t *counts, con
 
 int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sample_seed, uint64_t ply,
                 int64_t reset_seed, int32_t *counts, int32_t *offsets, int32_t *values, int64_t values_capacity,
-                int32_t *mask_words, int32_t obs_fmt, void *spatial, float *aux, float *global, uint8_t *terminated,
+                int32_t *mask_words, int32_t obs_fmt, void *spatial, void *aux, float *global, uint8_t *terminated,
                 float *reward, uint64_t *hash, int32_t *actions_out, void *stream)
 {
     int rc = check_env(e);
@@ -797,7 +799,7 @@ int jq_history_snapshot(jq_history *h, jq_env *e, const int8_t *acting, int32_t 
 }
 
 int jq_history_reconstruct(jq_history *h, const int64_t *flat, const int8_t *observer, int32_t batch, int32_t fmt,
-                           void *spatial, float *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
+                           void *spatial, void *aux, float *global, int32_t *mask_words, uint8_t *mask_bool,
                            void *stream)
 {
     if (!h) return fail(JQ_E_ARG, "null history");
@@ -894,7 +896,7 @@ int noalloc_state(int device, jq_env *&out)
 }  // namespace
 
 extern "C" int jq_history_reconstruct_noalloc(jq_history *h, const int64_t *flat, const int8_t *observer,
-                                              int32_t batch, int32_t fmt, void *spatial, float *aux, float *global,
+                                              int32_t batch, int32_t fmt, void *spatial, void *aux, float *global,
                                               int32_t *mask_words, uint8_t *mask_bool, void *stream)
 {
     if (!h) return fail(JQ_E_ARG, "null history");

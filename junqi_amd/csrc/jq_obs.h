@@ -18,8 +18,12 @@
 // iteration (a wave covers 1 KB of HBM), expands the chunk's bits to bytes
 // (u8), bf16 or f32, merges the image and issues one 16-byte store. Whether a
 // wave's 1 KB span touches an image range is decided once per wave.
-// The six continuous planes (turn history, recency) are exact floats: they go
-// to the aux output in the u8 format and are computed per element in f32 / bf16.
+// The six continuous planes (turn history, recency) are exact floats, computed
+// per element in f32 / bf16. The u8 format leaves them zero in the code planes
+// and writes one 2,320-byte aux row per observation instead: the two turn
+// history values as float32 (each is constant over its plane), then the four
+// recency planes as uint16 codes per cell, 0 for 0.0 and 1 + e for the value
+// exp(-e / tau) at elapsed step e (entry e of the recency table).
 //
 // The u8 kernel is persistent (grid = resident blocks): while a block streams
 // row i out, its threads already hold the gathered inputs of row i + gridDim.x
@@ -55,7 +59,9 @@ constexpr int STAT_Q0 = 130, STAT_NQ = 15;
 
 // continuous planes: 64-65 turn history, 253-256 recency
 constexpr int CT0_S = 64 * NC, CT0_E = 66 * NC, CT1_S = 253 * NC, CT1_E = 257 * NC;
-constexpr int AUX_ROW = 6 * NC;
+// u8 aux row: float32 turn history [2], then uint16 recency codes [4][289]
+constexpr int AUXC_ROW = 8 + 4 * NC * 2;   // 2,320 bytes
+static_assert(AUXC_ROW % 16 == 0, "aux rows must keep 16-byte alignment");
 
 // u8 codes of the fixed values (the decode table starts 0, 1, -1, 1/3, 2/3)
 constexpr uint8_t CODE_ONE = 1, CODE_NEG = 2, CODE_THIRD = 3, CODE_2THIRD = 4;
@@ -68,7 +74,10 @@ struct ObsLds {
     alignas(16) uint32_t bits[OBS_BITS_WORDS];
     alignas(16) uint8_t img[IMG_BYTES];
     alignas(16) uint32_t stat[STAT_NQ * 4];   // board_static words of `bits` (row-independent)
-    float rec[PID_STRIDE][4];        // recency values per pid (0 unless an enemy piece on board)
+    union {
+        float rec[PID_STRIDE][4];      // recency values per pid (0 unless an enemy piece on board): f32 / bf16
+        uint16_t rcode[PID_STRIDE][4]; // the same as aux codes (0 none, 1 + elapsed): u8
+    };
     float dec[32];                   // code -> f32
     uint32_t decb[32];               // code -> bf16 bits
     int8_t cpid[CELL_STRIDE];        // canonical cell -> pid (-1 empty)
@@ -179,10 +188,10 @@ __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int
 }
 
 // Scatter one pid's nonzero elements into bits / img.
-template <bool EXT = false>
+template <bool EXT = false, bool AUXC = false>
 __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, int m, const PieceIn &P,
-                                              const float rc[4], const uint32_t own_types[4], ObsLds &L,
-                                              const float *ext = nullptr, ExtLds *X = nullptr)
+                                              const float rc[4], const uint16_t rk[4], const uint32_t own_types[4],
+                                              ObsLds &L, const float *ext = nullptr, ExtLds *X = nullptr)
 {
     const int tm = (obs + 2) & 3, le = (obs + 1) & 3, team = obs & 1;
     const int s = pid / 30;
@@ -271,7 +280,10 @@ __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, i
             set_el(L, (161 + b) * NC + k);
         }
     }
-    for (int q = 0; q < 4; ++q) L.rec[pid][q] = rc[q];
+    for (int q = 0; q < 4; ++q) {
+        if (AUXC) L.rcode[pid][q] = rk[q];
+        else L.rec[pid][q] = rc[q];
+    }
 
     // death_reason (90-101) and dead_at_zero (102-103), observation.py:1103-1180
     if (P.dstep >= 0) {
@@ -314,6 +326,14 @@ __device__ __forceinline__ float recency_at(const State &S, int mc, int last, in
     int el = mc - last;
     el = el < 0 ? 0 : (el > 4095 ? 4095 : el);
     return S.rlut[q * 4096 + el];
+}
+
+__device__ __forceinline__ uint16_t recency_code(int mc, int last)
+{   // aux code of recency_at: 0 for no value, else 1 + the clamped elapsed step
+    if (last < 0) return 0;
+    int el = mc - last;
+    el = el < 0 ? 0 : (el > 4095 ? 4095 : el);
+    return (uint16_t)(1 + el);
 }
 
 // Row-independent LDS content (tables, board_static template) of one buffer.
@@ -406,23 +426,29 @@ __device__ __forceinline__ void row_fetch(const State &S, int env, int obs, int 
 // Fill a cleared buffer with row (env, obs) from the fetched inputs, thread t
 // in [0, 256). Only the recency-table gathers are loads here. No thread reads
 // what another one writes, so no barrier is needed inside.
-template <bool EXT = false>
+// AUXC (the u8 format): recency as aux codes, no table lookups.
+template <bool EXT = false, bool AUXC = false>
 __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, const RowIn &R, ObsLds &L,
                                          float *glob_row, const float *ext = nullptr, ExtLds *X = nullptr)
 {
     const int pid = t < PID_STRIDE ? piece_of_thread(t, obs) : -1;
     if (pid >= 0) {
         float rc[4] = {0.f, 0.f, 0.f, 0.f};
+        uint16_t rk[4] = {0, 0, 0, 0};
         if ((unsigned)R.P.pos < (unsigned)NC && t >= 64) {   // enemy pieces on the board
-            rc[0] = recency_at(S, R.mc, R.P.ldir, 0);
-            rc[1] = recency_at(S, R.mc, R.P.ldir, 1);
-            rc[2] = recency_at(S, R.mc, R.P.lchain, 2);
-            rc[3] = recency_at(S, R.mc, R.P.fstep, 3);
+            const int last[4] = {R.P.ldir, R.P.ldir, R.P.lchain, R.P.fstep};
+            for (int q = 0; q < 4; ++q) {
+                if (AUXC) rk[q] = recency_code(R.mc, last[q]);
+                else rc[q] = recency_at(S, R.mc, last[q], q);
+            }
         }
-        piece_scatter<EXT>(S.show_mode, obs, pid, m, R.P, rc, R.own_types, L, ext, X);
+        piece_scatter<EXT, AUXC>(S.show_mode, obs, pid, m, R.P, rc, rk, R.own_types, L, ext, X);
     } else if (t < PID_STRIDE) {   // the 8 spare threads clear the padding pids' recency
         const int pad = NP + (t < 64 ? t - 60 : t - 120);
-        for (int q = 0; q < 4; ++q) L.rec[pad][q] = 0.f;
+        for (int q = 0; q < 4; ++q) {
+            if (AUXC) L.rcode[pad][q] = 0;
+            else L.rec[pad][q] = 0.f;
+        }
     } else if (t < T_FLAGS) {   // move_history (129-160), observation.py:1207-1231
         const int cnt = R.hmeta & 0xFF, head = (R.hmeta >> 8) & 31;
         const int d = (head - 1 - (t - T_HIST)) & 31;   // plane of this ring slot (0 = most recent)
@@ -668,37 +694,38 @@ __device__ __forceinline__ uint4 u8_chunk(const ObsLds &L, int e0, int off)
                       nib_to_bytes(v >> 12) | b.w);
 }
 
-// Aux element e of a row: planes 64, 65 (turn history) then 253..256 (recency).
-__device__ __forceinline__ float aux_at(const ObsLds &L, int e)
+// Recency aux code j of a row (j = plane * 289 + canonical cell): the code of
+// the piece on that cell, 0 on an empty cell.
+__device__ __forceinline__ uint32_t rec_code_at(const ObsLds &L, int j)
 {
-    const int j = e / NC, k = e - j * NC;
-    return obs_cont_at(L, j < 2 ? 64 + j : 251 + j, k);
+    const int q = j / NC, k = j - q * NC;
+    const int pid = L.cpid[k];
+    return pid >= 0 ? L.rcode[pid][q] : 0u;
 }
 
-__device__ __forceinline__ uint4 aux_chunk(const ObsLds &L, int e0)
+// The 2,320-byte aux row of a u8 observation (16-byte aligned): thread ct < 145
+// writes bytes [16 ct, 16 ct + 16).
+__device__ __forceinline__ void obs_emit_aux_codes(const ObsLds &L, uint8_t *row, int ct)
 {
-    return make_uint4(__float_as_uint(aux_at(L, e0)), __float_as_uint(aux_at(L, e0 + 1)),
-                      __float_as_uint(aux_at(L, e0 + 2)), __float_as_uint(aux_at(L, e0 + 3)));
-}
-
-// The six continuous planes of a u8 row as float32 (6, 17, 17): one 16-byte
-// chunk per thread per iteration over the whole block.
-__device__ __forceinline__ void obs_emit_aux(const ObsLds &L, float *row, int ct)
-{
-    const int lead = (int)(((uintptr_t)row >> 2) & 3);          // elements before the first 16-byte line
-    const int qf = lead ? 1 : 0, ql = (AUX_ROW + lead) >> 2;    // full chunks [qf, ql)
-    for (int q = qf + ct; q < ql; q += OBS_THREADS) {
-        const int e0 = q * 4 - lead;
-        *reinterpret_cast<uint4 *>(row + e0) = aux_chunk(L, e0);
+    if (ct >= AUXC_ROW / 16) return;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = ct * 16 + i * 4;
+        if (b < 8) {
+            w[i] = __float_as_uint(L.turnv[b >> 2]);
+        } else {
+            const int j = (b - 8) >> 1;
+            w[i] = rec_code_at(L, j) | (rec_code_at(L, j + 1) << 16);
+        }
     }
-    if (ct == 128) for (int e = 0; e < (lead ? 4 - lead : 0); ++e) row[e] = aux_at(L, e);
-    if (ct == 192) for (int e = ql * 4 - lead; e < AUX_ROW; ++e) row[e] = aux_at(L, e);
+    *reinterpret_cast<uint4 *>(row + ct * 16) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // u8 row emission: the row's full 16-byte chunks, in 1 KB units of the output
-// buffer split into contiguous runs, one per wave. The aux planes follow,
-// spread over the block.
-__device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m, float *aux, int ct)
+// buffer split into contiguous runs, one per wave. The aux row follows, spread
+// over the block.
+__device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m, uint8_t *aux, int ct)
 {
     const int lead = m;
     const int qf = lead ? 1 : 0, ql = (OBS_ROW + lead) >> 4;   // full chunks [qf, ql)
@@ -730,7 +757,7 @@ __device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m
     // partial chunks at the two ends of the row
     if (ct == 0 && lead) obs_elems<2>(L, row, 0, 16 - m, m);
     if (ct == 64 && ((OBS_ROW + lead) & 15)) obs_elems<2>(L, row, ql * 16 - m, OBS_ROW, m);
-    if (aux) obs_emit_aux(L, aux, ct);
+    if (aux) obs_emit_aux_codes(L, aux, ct);
 }
 
 // nrows = N (one row per env, observer given or the acting seat) or 4N
@@ -739,7 +766,7 @@ __device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m
 // beliefs per (env, observer).
 template <int FMT, bool EXT = false>
 __global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *__restrict__ observer, int all_seats,
-                                                         void *__restrict__ spatial, float *__restrict__ aux,
+                                                         void *__restrict__ spatial, void *__restrict__ aux,
                                                          float *__restrict__ glob, int nrows,
                                                          const float *__restrict__ ext = nullptr)
 {
@@ -761,10 +788,10 @@ __global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *
     lds_barrier();
     RowIn R;
     row_fetch(S, env, obs, t, R);
-    row_fill<EXT>(S, obs, m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr,
-                  EXT ? ext + ((size_t)env * 4 + obs) * 12 * NC : nullptr, X);
+    row_fill<EXT, FMT == 2>(S, obs, m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr,
+                            EXT ? ext + ((size_t)env * 4 + obs) * 12 * NC : nullptr, X);
     lds_barrier();
-    if (FMT == 2) obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUX_ROW : nullptr, t);
+    if (FMT == 2) obs_emit_u8(L, rowp, m, aux ? static_cast<uint8_t *>(aux) + (size_t)row * AUXC_ROW : nullptr, t);
     else obs_emit<FMT, EXT>(L, rowp, m, X);
 }
 
@@ -773,7 +800,7 @@ __global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *
 // (in flight during the stores), stream the row, clear the buffer.
 __global__ __launch_bounds__(OBS_THREADS) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_observe_u8_persist(
     State S, const int8_t *__restrict__ observer, int all_seats, uint8_t *__restrict__ spatial,
-    float *__restrict__ aux, float *__restrict__ glob, int nrows)
+    uint8_t *__restrict__ aux, float *__restrict__ glob, int nrows)
 {
     __shared__ ObsLds L;
     const int t = threadIdx.x, G = gridDim.x;
@@ -786,10 +813,11 @@ __global__ __launch_bounds__(OBS_THREADS) __attribute__((amdgpu_waves_per_eu(4, 
     for (int row = blockIdx.x; row < nrows; row += G) {
         uint8_t *rowp = spatial + (size_t)row * OBS_ROW;
         const int m = (int)((uintptr_t)rowp & 15);
-        row_fill(S, row_obs(S, observer, all_seats, row), m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr);
+        row_fill<false, true>(S, row_obs(S, observer, all_seats, row), m, t, R, L,
+                              glob ? glob + (size_t)row * 28 : nullptr);
         lds_barrier();
         if (row + G < nrows) row_fetch(S, row_env(row + G, all_seats), row_obs(S, observer, all_seats, row + G), t, R);
-        obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUX_ROW : nullptr, t);
+        obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUXC_ROW : nullptr, t);
         lds_barrier();
         obs_clear(L, t, OBS_THREADS);
         lds_barrier();

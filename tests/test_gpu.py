@@ -135,12 +135,12 @@ def test_obs_formats_agree(jq):
     u8, gu8, aux = b.observe(fmt="u8")
     f32 = f32.cpu().numpy()
     assert np.array_equal(bf.view(torch.int16).cpu().numpy().view(np.uint16), _bf16_rne(f32))
-    dec = jq.decode_table()[u8.cpu().numpy()]
-    aux = aux.cpu().numpy()
-    for j, ch in enumerate(jq.AUX_CHANNELS):
-        assert np.all(dec[:, ch] == 0)
-        dec[:, ch] = aux[:, j]
+    u8n = u8.cpu().numpy()
+    for ch in jq.AUX_CHANNELS:
+        assert np.all(u8n[:, ch] == 0)
+    dec = jq.decode_u8(u8n, aux.cpu().numpy())
     assert np.array_equal(dec.view(np.uint32), f32.view(np.uint32))
+    assert torch.equal(jq.decode_u8(u8, aux).cpu(), torch.from_numpy(dec))   # the device decode too
     assert np.array_equal(g32.cpu().numpy(), gu8.cpu().numpy())
     b.close()
 
@@ -461,7 +461,7 @@ def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt, given, show
     b.legal()
     u8 = fmt == "u8"
     sp = torch.empty((n, 317, 17, 17), dtype=torch.uint8 if u8 else torch.float32, device=b.device)
-    aux = torch.empty((n, 6, 17, 17), dtype=torch.float32, device=b.device) if u8 else None
+    aux = torch.empty((n, jq._lib.AUX_BYTES), dtype=torch.uint8, device=b.device) if u8 else None
     gl = torch.empty((n, 28), dtype=torch.float32, device=b.device)
     term = torch.empty(n, dtype=torch.uint8, device=b.device)
     rew = torch.empty(n, dtype=torch.float32, device=b.device)
@@ -509,9 +509,7 @@ def test_env_step_fused_matches_oracle(jq, max_moves, plies, n, fmt, given, show
             assert np.array_equal(mw[i], G.canonical_mask_words(ids, int(g.turn), tables)), (ply, i)
             osp, ogl = g.observe(int(g.turn))
             if u8:
-                d = dec[spn[i]]
-                for j, ch in enumerate(jq.AUX_CHANNELS):
-                    d[ch] = ax[i, j]
+                d = jq.decode_u8(spn[i], ax[i])
             else:
                 d = spn[i]
             assert np.array_equal(d.view(np.uint32), osp.view(np.uint32)), (ply, i)

@@ -148,7 +148,7 @@ def test_c3_mixed_stage_observations_16384(jq, show_mode):
     assert mc.min() <= 10 and mc.max() >= 390, (mc.min(), mc.max())
     dec = jq.decode_table()
     sp8 = torch.empty((n, 317, 17, 17), dtype=torch.uint8, device=b.device)
-    aux = torch.empty((n, 6, 17, 17), dtype=torch.float32, device=b.device)
+    aux = torch.empty((n, jq._lib.AUX_BYTES), dtype=torch.uint8, device=b.device)
     gl8 = torch.empty((n, 28), dtype=torch.float32, device=b.device)
     for extra in range(2):
         k = warm + extra
@@ -162,10 +162,7 @@ def test_c3_mixed_stage_observations_16384(jq, show_mode):
             osp, ogl = O.batch_observe(ob, g0, g1)
             u8 = sp8[g0:g1].cpu().numpy()
             assert int(u8.max()) < 32, "u8 code outside the decode table"
-            got = dec[u8]
-            a = aux[g0:g1].cpu().numpy()
-            for j, c in enumerate(jq.AUX_CHANNELS):
-                got[:, c] = a[:, j]
+            got = jq.decode_u8(u8, aux[g0:g1].cpu().numpy())
             assert np.array_equal(got, osp), f"c3 u8 observation, games {g0}-{g1}, ply {k}"
             assert np.array_equal(gl8[g0:g1].cpu().numpy(), ogl)
             if sp16 is not None:
@@ -204,7 +201,7 @@ def test_c5_rollout_32768(jq):
     start = np.random.default_rng(5).integers(0, warm, n).astype(np.int32)
     dev = b.device
     obs = (torch.empty((n, 317, 17, 17), dtype=torch.uint8, device=dev),
-           torch.empty((n, 6, 17, 17), dtype=torch.float32, device=dev),
+           torch.empty((n, jq._lib.AUX_BYTES), dtype=torch.uint8, device=dev),
            torch.empty((n, 28), dtype=torch.float32, device=dev))
     got = _drive(b, steps, sampler="logits", seed=seed, active_from=start, obs_from=warm, obs=obs)
     ob = O.Batch(jq.generate_lineups(505, n), show_mode=2)
@@ -218,10 +215,7 @@ def test_c5_rollout_32768(jq):
     assert int(u8.max()) < 32
     osp, ogl = O.batch_observe(ob, 0, 1024)
     dec = jq.decode_table()
-    gotsp = dec[u8[:1024].cpu().numpy()]
-    a = obs[1][:1024].cpu().numpy()
-    for j, c in enumerate(jq.AUX_CHANNELS):
-        gotsp[:, c] = a[:, j]
+    gotsp = jq.decode_u8(u8[:1024].cpu().numpy(), obs[1][:1024].cpu().numpy())
     assert np.array_equal(gotsp, osp)
     assert np.array_equal(obs[2][:1024].cpu().numpy(), ogl)
     b.close()

@@ -46,7 +46,7 @@ def _run(jq, plies, sample, check):
     b.legal()
     dev = b.device
     sp = torch.empty((N, 317, 17, 17), dtype=torch.uint8, device=dev)
-    aux = torch.empty((N, 6, 17, 17), dtype=torch.float32, device=dev)
+    aux = torch.empty((N, jq._lib.AUX_BYTES), dtype=torch.uint8, device=dev)
     gl = torch.empty((N, 28), dtype=torch.float32, device=dev)
     term = torch.empty(N, dtype=torch.uint8, device=dev)
     rew = torch.empty(N, dtype=torch.float32, device=dev)
@@ -108,9 +108,7 @@ def _run(jq, plies, sample, check):
             assert np.array_equal(vals[offs[i]:offs[i + 1]], ids), (ply, i)
             assert np.array_equal(mw[j], G.canonical_mask_words(ids, int(g.turn), tables)), (ply, i)
             osp, ogl = g.observe(int(g.turn))
-            d = dec[u8[j]]
-            for k, ch in enumerate(jq.AUX_CHANNELS):
-                d[ch] = ax[j, k]
+            d = jq.decode_u8(u8[j], ax[j])
             assert np.array_equal(d.view(np.uint32), osp.view(np.uint32)), (ply, i)
             assert np.array_equal(g2[j], ogl), (ply, i)
     return b, games, np.stack(digest)

@@ -25,7 +25,7 @@ def jq():
 def _outputs(dev, batch, fmt):
     dt = {"f32": torch.float32, "u8": torch.uint8}[fmt]
     return {"spatial": torch.full((batch, 317, 17, 17), 7, dtype=dt, device=dev),
-            "aux": torch.full((batch, 6, 17, 17), 7, dtype=torch.float32, device=dev) if fmt == "u8" else None,
+            "aux": torch.full((batch, 2320), 7, dtype=torch.uint8, device=dev) if fmt == "u8" else None,
             "global": torch.full((batch, 28), 7, dtype=torch.float32, device=dev),
             "mask_words": torch.full((batch, 521), 7, dtype=torch.int32, device=dev),
             "mask_bool": torch.full((batch, 16641), 7, dtype=torch.uint8, device=dev)}
