@@ -1,10 +1,20 @@
 """Throughput of the batched Junqi env-step on one MI355X.
 
-One step = for every game: draw an action uniformly from its legal row
-(Philox4x32-10), apply the ply, auto-reset finished games from the setup pool,
-generate the next acting seat's legal actions (sorted CSR + packed canonical
-mask) and its 317-plane observation (u8 codes + aux rows + 28 globals).
-Prints one JSON line. Usage: python bench.py [--steps K] [--warmup W] [--envs N]
+One env-step = for every game: draw an action (masked N(0,1)-logit argmax over
+the legal canonical ids, Philox4x32-10), apply the ply, restart a finished game
+from the setup pool, generate the next acting seat's legal actions (sorted CSR
++ packed canonical mask) and its 317-plane observation (u8 codes + aux row +
+28 globals), and record reward, done and Zobrist hash. That is the rollout loop
+of the 32,768-game configuration; before timing, the batch is played into mixed
+stages (game i starts S_i steps late, S_i uniform below --stagger), so the
+timed window holds openings, middle games and endgames, and games end and
+restart inside it.
+
+Prints one JSON line. Usage: python bench.py [--steps K] [--warmup W]
+  --config c5 (default): 32,768 games, logits sampler, step + CSR + mask + u8 obs
+  --config c3: 16,384 games at plies 0-400, uniform sampler, step + CSR + mask + obs
+  --config c2: 4,096 games, uniform sampler, step + CSR + mask (no observation)
+  --path fused | separate | dropin (the reference collector's GpuRollout calls)
 """
 
 from __future__ import annotations
@@ -12,6 +22,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -20,10 +31,17 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-OBS_U8_BYTES = 317 * 289          # 91,613
+OBS_ELEMS = 317 * 289             # 91,613 elements per observation
 AUX_BYTES = 8 + 4 * 289 * 2       # 2,320: turn history f32[2] + recency codes u16[4][289]
 GLOBAL_BYTES = 28 * 4             # 112
-MASK_BYTES = 521 * 4              # 2,084
+MASK_BYTES = 521 * 4              # 2,084 packed canonical mask
+STEP_OUT_BYTES = 1 + 4 + 8 + 4    # terminated, reward, hash, action per env
+METRIC = "env-steps/sec incl. legal mask + obs at 32768 games on 1 MI355X; % HBM peak"
+CONFIGS = {
+    "c5": dict(envs=32768, sampler="logits", obs=True, stagger=800),
+    "c3": dict(envs=16384, sampler="uniform", obs=True, stagger=401),
+    "c2": dict(envs=4096, sampler="uniform", obs=False, stagger=800),
+}
 
 
 def parse():
@@ -31,14 +49,18 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--envs", type=int, default=32768)
+    ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
+    ap.add_argument("--envs", type=int, default=0, help="override the config's game count")
     ap.add_argument("--fmt", default="u8", choices=["u8", "bf16", "f32"])
-    ap.add_argument("--path", default="fused", choices=["fused", "separate"],
-                    help="fused: jq_env_step; separate: the same step through jq_sample_uniform, jq_step, "
-                         "jq_reset_terminated and jq_legal, the reference collector's call order")
+    ap.add_argument("--sampler", default="", choices=["", "logits", "uniform"])
+    ap.add_argument("--stagger", type=int, default=-1, help="mixed-stage warm-up steps (0 = all games fresh)")
+    ap.add_argument("--show-mode", type=int, default=2, choices=[0, 1, 2])
+    ap.add_argument("--path", default="fused", choices=["fused", "separate", "dropin"],
+                    help="fused: jq_env_step; separate: jq_sample_* + jq_step + jq_reset_terminated + jq_legal; "
+                         "dropin: GpuRollout's f32 observation, bool mask, canonical step and device reset")
     ap.add_argument("--seed", type=int, default=0x4A51)
-    ap.add_argument("--cpu-envs", type=int, default=4096)
-    ap.add_argument("--cpu-steps", type=int, default=40)
+    ap.add_argument("--cpu-envs", type=int, default=2048)
+    ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (counter calibration) and exit")
@@ -60,46 +82,47 @@ def calibrate_copy(mb: int) -> int:
     return 0
 
 
-def cpu_baseline(envs: int, steps: int) -> dict:
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(envs: int, steps: int, sampler: int, obs: bool, seed: int) -> dict:
     """The C oracle (a scalar port, OpenMP over games) on this host's cores, on a
-    bounded sample of the same workload: step + sorted legal ids + canonical mask
-    + float32 observation of the acting seat."""
+    bounded sample of the same workload: sample -> step -> pool restart -> sorted
+    legal ids + canonical mask (+ float32 observation of the acting seat), games
+    first played into mixed stages; once on every host thread and once on one."""
     import numpy as np
 
     from oracle import oracle as O
 
     setups = np.stack([O.random_setup(i) for i in range(envs)])
-    batch = O.Batch(setups, show_mode=2)
-    sp = np.zeros((envs, 317, 17, 17), np.float32)
-    gl = np.zeros((envs, 28), np.float32)
-    mask = np.zeros((envs, 2081), np.uint8)
-    rng = np.random.default_rng(0)
-    none = np.full(envs, -1, np.int32)
-    batch.env_step(none, obs=True, mask_bits=mask, obs_spatial=sp, obs_global=gl)
+    env = O.CpuEnv(setups, O.setup_pool(42, 1000))
+    for k in range(64):   # leave the opening: games spread over plies 0-64
+        env.step(k, sampler=sampler, seed=seed, obs=False)
+    all_threads = O.omp_threads()
 
-    def pick():
-        acts = np.full(envs, -1, np.int32)
-        for i in range(envs):
-            g = batch.games[i]
-            if g["terminated"]:
-                continue
-            # any legal action will do for timing; use the oracle's own generator
-            ids = np.zeros(4096, np.int32)
-            n = O.lib().jqo_legal_ids(batch.games[i:i + 1].ctypes.data, int(g["turn"]), ids.ctypes.data, 4096)
-            if n > 0:
-                acts[i] = ids[rng.integers(n)]
-        return acts
-
-    total = 0.0
-    for _ in range(steps):
-        acts = pick()
+    def timed(nsteps: int, k0: int) -> float:
+        env.step(k0, sampler=sampler, seed=seed, obs=obs)   # first touch of the output pages
         t0 = time.perf_counter()
-        batch.env_step(acts, obs=True, mask_bits=mask, obs_spatial=sp, obs_global=gl)
-        total += time.perf_counter() - t0
-    return {"value": round(envs * steps / total, 1), "unit": "env-steps/s", "cores": O.omp_threads(),
-            "kind": "port",
-            "sample": f"{envs} games x {steps} env-steps (step + legal ids + canonical mask + f32 obs), "
-                      f"random legal actions, HALF_DARK"}
+        for k in range(nsteps):
+            env.step(k0 + 1 + k, sampler=sampler, seed=seed, obs=obs)
+        return envs * nsteps / (time.perf_counter() - t0)
+
+    v_all = timed(steps, 100)
+    O.set_threads(1)
+    v_one = timed(max(1, steps // 4), 200)
+    O.set_threads(all_threads)
+    work = "step + sorted legal ids + canonical mask" + (" + f32 obs" if obs else "")
+    return {"value": round(v_all, 1), "unit": "env-steps/s", "cores": all_threads, "kind": "port",
+            "single_core_value": round(v_one, 1), "cpu_model": cpu_model(),
+            "sample": f"{envs} games x {steps} env-steps on {all_threads} threads and {envs} x {max(1, steps // 4)} "
+                      f"on 1 ({work}, {'logits' if sampler else 'uniform'} sampler, HALF_DARK, after 64 untimed steps)"}
 
 
 # device kernel that writes the observation rows, per output format
@@ -110,10 +133,10 @@ def measured_traffic(kernel: str, games: int):
     """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, scaled against a
     plain copy) from the committed counter summary, when it was taken at this size."""
     path = ROOT / "profiles" / "traffic.json"
-    if games != 32768 or not path.exists():
+    if not path.exists():
         return None
     rec = json.loads(path.read_text()).get("kernels", {}).get(kernel)
-    if not rec:
+    if not rec or rec.get("games") != games:
         return None
     return round(rec["read_bytes"] + rec["write_bytes"])
 
@@ -132,98 +155,156 @@ def main() -> int:
     import junqi_amd
     from junqi_amd import _lib as L
 
-    n = args.envs
-    b = junqi_amd.JunqiBatch(n, show_mode=2, max_num_moves=4000, pool_size=10000)
-    dev = b.device
+    cfg = dict(CONFIGS[args.config])
+    n = args.envs or cfg["envs"]
+    sampler = args.sampler or cfg["sampler"]
+    smp = L.SAMPLE_LOGITS if sampler == "logits" else L.SAMPLE_UNIFORM
+    stagger = cfg["stagger"] if args.stagger < 0 else args.stagger
+    with_obs = cfg["obs"] or args.path == "dropin"
+    fmt = "f32" if args.path == "dropin" else args.fmt
+    b = junqi_amd.JunqiBatch(n, show_mode=args.show_mode, max_num_moves=4000, pool_size=10000)
     b.reset(0)
     b.legal()
-    es = {"u8": 1, "bf16": 2, "f32": 4}[args.fmt]
-    sdt = {"u8": torch.uint8, "bf16": torch.bfloat16, "f32": torch.float32}[args.fmt]
-    spatial = torch.empty((n, 317, 17, 17), dtype=sdt, device=dev)
-    aux = torch.empty((n, AUX_BYTES), dtype=torch.uint8, device=dev) if args.fmt == "u8" else None
-    glob = torch.empty((n, 28), dtype=torch.float32, device=dev)
-    term = torch.empty(n, dtype=torch.uint8, device=dev)
-    reward = torch.empty(n, dtype=torch.float32, device=dev)
-    acts = torch.empty(n, dtype=torch.int32, device=dev)
-    fmt_code = {"u8": L.OBS_U8, "bf16": L.OBS_BF16, "f32": L.OBS_F32}[args.fmt]
-    h = b._h
-    lib = L.lib
+    dev = b.device
+    es = {"u8": 1, "bf16": 2, "f32": 4}[fmt]
+    sdt = {"u8": torch.uint8, "bf16": torch.bfloat16, "f32": torch.float32}[fmt]
+    fmt_code = {"u8": L.OBS_U8, "bf16": L.OBS_BF16, "f32": L.OBS_F32}[fmt]
+    spatial = torch.empty((n, 317, 17, 17), dtype=sdt, device=dev) if with_obs else None
+    aux = torch.empty((n, AUX_BYTES), dtype=torch.uint8, device=dev) if with_obs and fmt == "u8" else None
+    glob = torch.empty((n, 28), dtype=torch.float32, device=dev) if with_obs else None
+    K = args.steps
+    term = torch.empty((K + 1, n), dtype=torch.uint8, device=dev)
+    reward = torch.empty((K + 1, n), dtype=torch.float32, device=dev)
+    hsh = torch.empty((K + 1, n), dtype=torch.int64, device=dev)
+    acts = torch.empty((K + 1, n), dtype=torch.int32, device=dev)
+    canon = torch.empty(n, dtype=torch.int32, device=dev)
+    mask_bool = torch.empty((n, 16641), dtype=torch.uint8, device=dev) if args.path == "dropin" else None
+    h, lib = b._h, L.lib
+    cap = b.values.numel()
     P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
 
-    def one_step(ply: int, ev_obs=None):
+    # ---- mixed stages: game i takes no action during its first S_i steps
+    start = torch.from_numpy(np.random.default_rng(7).integers(0, max(1, stagger), n).astype(np.int64)).to(dev)
+    for k in range(stagger):
         s = torch.cuda.current_stream(dev).cuda_stream
-        # Philox pick from the previous CSR rows, ply, restart from the pool,
-        # next seat's sorted CSR + packed canonical mask (jq_env_step without
-        # the observation, which is launched on its own so events can time it)
-        if args.path == "fused":
-            L.check(lib.jq_env_step(h, None, L.SAMPLE_UNIFORM, args.seed, ply, ply, b.counts.data_ptr(),
-                                    b.offsets.data_ptr(), b.values.data_ptr(), b.values.numel(),
-                                    b.mask_words.data_ptr(), fmt_code, None, None, None, term.data_ptr(),
-                                    reward.data_ptr(), None, acts.data_ptr(), s))
+        a = acts[0]
+        if smp == L.SAMPLE_LOGITS:
+            L.check(lib.jq_sample_logits(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
+                                         cap, args.seed, k, a.data_ptr(), None, s))
         else:
-            L.check(lib.jq_sample_uniform(h, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
-                                          b.values.numel(), args.seed, ply, acts.data_ptr(), s))
-            L.check(lib.jq_step(h, acts.data_ptr(), None, L.ACT_WORLD, None, None, term.data_ptr(), None, None,
-                                None, None, reward.data_ptr(), None, s))
+            L.check(lib.jq_sample_uniform(h, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(), cap,
+                                          args.seed, k, a.data_ptr(), s))
+        a.copy_(torch.where(start > k, torch.full_like(a, -1), a))
+        L.check(lib.jq_env_step(h, a.data_ptr(), smp, args.seed, k, k, b.counts.data_ptr(), b.offsets.data_ptr(),
+                                b.values.data_ptr(), cap, b.mask_words.data_ptr(), fmt_code, None, None, None,
+                                None, None, None, None, s))
+    torch.cuda.synchronize(dev)
+    plies0 = b.get_field("move_counter")[:, 0]
+
+    def one_step(ply: int, slot: int, ev_obs=None):
+        s = torch.cuda.current_stream(dev).cuda_stream
+        if args.path == "fused":
+            # sample from the previous CSR rows, ply, restart, next seat's CSR + mask;
+            # the observation is launched on its own so events can time its kernel
+            L.check(lib.jq_env_step(h, None, smp, args.seed, ply, ply, b.counts.data_ptr(), b.offsets.data_ptr(),
+                                    b.values.data_ptr(), cap, b.mask_words.data_ptr(), fmt_code, None, None, None,
+                                    term[slot].data_ptr(), reward[slot].data_ptr(), hsh[slot].data_ptr(),
+                                    acts[slot].data_ptr(), s))
+        elif args.path == "separate":
+            if smp == L.SAMPLE_LOGITS:
+                L.check(lib.jq_sample_logits(h, None, b.counts.data_ptr(), b.offsets.data_ptr(),
+                                             b.values.data_ptr(), cap, args.seed, ply, acts[slot].data_ptr(), None, s))
+            else:
+                L.check(lib.jq_sample_uniform(h, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
+                                              cap, args.seed, ply, acts[slot].data_ptr(), s))
+            L.check(lib.jq_step(h, acts[slot].data_ptr(), None, L.ACT_WORLD, None, None, term[slot].data_ptr(),
+                                None, None, None, None, reward[slot].data_ptr(), None, s))
             L.check(lib.jq_reset_terminated(h, ply, s))
-            L.check(lib.jq_legal(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
-                                 b.values.numel(), b.mask_words.data_ptr(), None, s))
-        if ev_obs is not None:
-            ev_obs[0].record()
-        L.check(lib.jq_observe(h, None, fmt_code, 0, spatial.data_ptr(), P(aux), glob.data_ptr(), s))
-        if ev_obs is not None:
-            ev_obs[1].record()
+            L.check(lib.jq_legal(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(), cap,
+                                 b.mask_words.data_ptr(), None, s))
+        else:   # GpuRollout's calls: canonical step of the acting seats, device reset, bool mask + CSR
+            turn = b.field_tensor("turn").contiguous()   # turn_torch(): the acting seats
+            L.check(lib.jq_sample_logits(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(),
+                                         cap, args.seed, ply, acts[slot].data_ptr(), canon.data_ptr(), s))
+            L.check(lib.jq_step(h, canon.data_ptr(), turn.data_ptr(), L.ACT_CANONICAL, None, None,
+                                term[slot].data_ptr(), None, None, None, None, reward[slot].data_ptr(), None, s))
+            L.check(lib.jq_reset_terminated(h, ply, s))
+            L.check(lib.jq_legal(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(), cap,
+                                 None, mask_bool.data_ptr(), s))
+        if with_obs:
+            if ev_obs is not None:
+                ev_obs[0].record()
+            L.check(lib.jq_observe(h, None, fmt_code, 0, spatial.data_ptr(), P(aux), glob.data_ptr(), s))
+            if ev_obs is not None:
+                ev_obs[1].record()
 
     for w in range(args.warmup):
-        one_step(w)
+        one_step(stagger + w, K)
     torch.cuda.synchronize(dev)
     obs_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(args.steps)]
+                  for _ in range(K)] if with_obs else [None] * K
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(dev)
     wall0 = time.perf_counter()
     t_start.record()
-    for k in range(args.steps):
-        one_step(args.warmup + k, obs_events[k])
+    for k in range(K):
+        one_step(stagger + args.warmup + k, k, obs_events[k])
     t_end.record()
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
     ms_total = t_start.elapsed_time(t_end)
-    obs_ms = sum(a.elapsed_time(c) for a, c in obs_events) / args.steps
-    legal_total = int(b.offsets[-1].item())
+    obs_ms = sum(a.elapsed_time(c) for a, c in obs_events) / K if with_obs else None
+    kbar = int(b.offsets[-1].item()) / n
+    ended = int(term[:K].sum().item())
 
-    steps_per_s = n * args.steps / (ms_total / 1e3)
-    obs_bytes = n * (OBS_U8_BYTES * es + (AUX_BYTES if args.fmt == "u8" else 0) + GLOBAL_BYTES)
-    achieved = obs_bytes / (obs_ms / 1e3) / 1e9
-    kbar = legal_total / n
+    steps_per_s = n * K / (ms_total / 1e3)
+    obs_bytes = (OBS_ELEMS * es + (AUX_BYTES if fmt == "u8" else 0) + GLOBAL_BYTES) if with_obs else 0
+    mask_bytes = 16641 if args.path == "dropin" else MASK_BYTES
+    step_bytes = obs_bytes + mask_bytes + 8 + 4 * kbar + (STEP_OUT_BYTES if args.path == "fused" else 5)
+    whole = step_bytes * steps_per_s / 1e9
     rec = {
-        "metric": "env-steps/sec incl. legal mask + obs at 32768 games on 1 MI355X; % HBM peak",
+        "metric": METRIC,
         "value": round(steps_per_s, 1),
         "unit": "env-steps/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_total / args.steps, 4),
+        "ms_per_step": round(ms_total / K, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8" if args.fmt == "u8" else args.fmt,
-        "data": "synthetic: seeded random legal setups, Philox-uniform legal actions, auto-reset from a 10000-setup pool",
-        "config": {"workload": f"step + sorted legal CSR + packed canonical mask + 317-plane {args.fmt} obs "
-                               f"of the acting seat, {n} games, HALF_DARK", "games": n, "obs_format": args.fmt,
-                   "path": args.path,
-                   "mean_legal_actions": round(kbar, 2)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(OBS_KERNEL[args.fmt], n),
-                     "kernel": OBS_KERNEL[args.fmt], "kernel_ms": round(obs_ms, 4),
-                     "bytes_per_launch": obs_bytes},
+        "dtype": fmt if with_obs else "int32",
+        "data": "synthetic: seeded random legal setups, Philox-sampled legal actions, games played into mixed "
+                "stages before timing, auto-reset from a 10000-setup pool",
+        "config": {"workload": f"{args.config}: sample ({sampler}) + step + pool restart + sorted legal CSR + "
+                               + ("bool canonical mask" if args.path == "dropin" else "packed canonical mask")
+                               + (f" + 317-plane {fmt} obs of the acting seat" if with_obs else "")
+                               + f", {n} games, show mode {args.show_mode}",
+                   "games": n, "obs_format": fmt if with_obs else None, "path": args.path, "sampler": sampler,
+                   "stagger_steps": stagger, "mean_legal_actions": round(kbar, 2),
+                   "plies_at_start": {"min": int(plies0.min()), "mean": round(float(plies0.mean()), 1),
+                                      "max": int(plies0.max())},
+                   "games_ended_in_window": ended},
+        "whole_step": {"bytes_per_env_step": round(step_bytes, 1), "achieved_GBps": round(whole, 1),
+                       "frac": round(whole / HBM_PEAK_GBS, 4)},
         "wall_s": round(wall, 3),
     }
-    if not args.no_cpu:
-        rec["cpu_baseline"] = cpu_baseline(args.cpu_envs, args.cpu_steps)
-    print(json.dumps(rec), flush=True)
+    if with_obs:
+        per_launch = n * obs_bytes
+        achieved = per_launch / (obs_ms / 1e3) / 1e9
+        rec["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(achieved / HBM_PEAK_GBS, 4),
+                           "traffic": measured_traffic(OBS_KERNEL[fmt], n),
+                           "kernel": OBS_KERNEL[fmt], "kernel_ms": round(obs_ms, 4), "bytes_per_launch": per_launch}
+    else:
+        rec["roofline"] = {"bound": "hbm", "achieved": round(whole, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(whole / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "whole step",
+                           "kernel_ms": round(ms_total / K, 4), "bytes_per_launch": round(step_bytes * n)}
     b.close()
+    if not args.no_cpu:
+        rec["cpu_baseline"] = cpu_baseline(args.cpu_envs, args.cpu_steps, 1 if sampler == "logits" else 0,
+                                           with_obs, args.seed)
+    print(json.dumps(rec), flush=True)
     return 0
 
 

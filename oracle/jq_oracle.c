@@ -1511,3 +1511,60 @@ void jqo_batch_observe(const jqo_game *gs, int g0, int g1, float *spatial, float
         jqo_observe(&gs[i], gs[i].turn, spatial + (size_t)(i - g0) * JQO_OBS_C * NC,
                     glob + (size_t)(i - g0) * JQO_OBS_G);
 }
+
+/* The CPU baseline's env-step (OpenMP over games): each game draws its action
+ * from the legal ids the previous call left in ids[i] (row cap `cap`, count
+ * counts[i]) with `sampler` (0 uniform, 1 masked logits) under (seed, ply),
+ * applies it, restarts from pool[jqo_reset_pool_index(i, reset_seed)] when it
+ * ended, then writes the new acting seat's legal ids and count, its packed
+ * canonical mask (mask_bits: n x 2081 bytes, may be NULL) and its float32
+ * observation (obs_spatial / obs_global, may be NULL). Call once with
+ * ply < 0 to fill the ids of the opening positions without stepping.
+ * Returns the total legal-id count. */
+long jqo_batch_cpu_env_step(jqo_game *gs, int n, const int8_t *pool, int pool_size, int sampler, uint64_t seed,
+                            int64_t ply, int64_t reset_seed, int32_t *ids, int cap, int32_t *counts,
+                            uint8_t *mask_bits, float *obs_spatial, float *obs_global)
+{
+    long total = 0;
+#pragma omp parallel for schedule(dynamic, 16) reduction(+:total)
+    for (int i = 0; i < n; i++) {
+        jqo_game *g = &gs[i];
+        int32_t *row = ids + (size_t)i * cap;
+        if (ply >= 0) {
+            int m = counts[i], seat = g->turn;
+            int32_t a = sampler ? jqo_sample_logits(row, m, seat, i, seed, (uint64_t)ply, NULL)
+                                : jqo_sample_uniform(row, m, i, seed, (uint64_t)ply);
+            jqo_result r;
+            if (a >= 0) jqo_step(g, a / NC, a % NC, &r);
+            if (g->terminated && pool && pool_size > 0)
+                jqo_new_game(g, pool + (size_t)jqo_reset_pool_index(i, reset_seed, pool_size) * 120, g->show_mode,
+                             g->max_num_moves);
+        }
+        int32_t tmp[4096];
+        int k = jqo_legal_ids(g, g->turn, tmp, 4096);
+        if (k > cap) k = cap;
+        memcpy(row, tmp, sizeof(int32_t) * (size_t)k);
+        counts[i] = k;
+        total += k;
+        if (mask_bits) {
+            uint8_t *bits = mask_bits + (size_t)i * 2081;
+            memset(bits, 0, 2081);
+            for (int j = 0; j < k; j++) {
+                int bit = jqo_canonical_id(g->turn, row[j]);
+                bits[bit >> 3] |= (uint8_t)(1u << (bit & 7));
+            }
+        }
+        if (obs_spatial && obs_global)
+            jqo_observe(g, g->turn, obs_spatial + (size_t)i * JQO_OBS_C * NC, obs_global + (size_t)i * JQO_OBS_G);
+    }
+    return total;
+}
+
+void jqo_set_threads(int n)
+{
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}

@@ -176,6 +176,14 @@ long jqo_batch_rollout(jqo_game *gs, int n, const int8_t *pool, int pool_size, i
                        uint64_t ply0, int64_t reset_seed0, int steps, const int32_t *active_from, float *reward,
                        uint8_t *done, uint64_t *hash, int32_t *actions, int32_t *legal_count,
                        uint64_t *legal_digest);
+/* The CPU baseline's env-step: sample from the ids left by the previous call,
+ * step, restart from the pool, new legal ids + canonical mask + f32 observation
+ * (OpenMP over games; ply < 0 only fills the opening ids). */
+long jqo_batch_cpu_env_step(jqo_game *gs, int n, const int8_t *pool, int pool_size, int sampler, uint64_t seed,
+                            int64_t ply, int64_t reset_seed, int32_t *ids, int cap, int32_t *counts,
+                            uint8_t *mask_bits, float *obs_spatial, float *obs_global);
+/* OpenMP thread count of the batch functions (n > 0). */
+void jqo_set_threads(int n);
 /* Acting-seat observations of games [g0, g1), rows from 0 (OpenMP). */
 void jqo_batch_observe(const jqo_game *gs, int g0, int g1, float *spatial, float *glob);
 

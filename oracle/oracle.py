@@ -119,6 +119,9 @@ def lib() -> C.CDLL:
     L.jqo_batch_rollout.argtypes = [P, I, P, I, I, C.c_uint64, C.c_uint64, C.c_int64, I, P, P, P, P, P, P, P]
     L.jqo_batch_rollout.restype = C.c_long
     L.jqo_batch_observe.argtypes = [P, I, I, P, P]
+    L.jqo_batch_cpu_env_step.argtypes = [P, I, P, I, I, C.c_uint64, C.c_int64, C.c_int64, P, I, P, P, P, P]
+    L.jqo_batch_cpu_env_step.restype = C.c_long
+    L.jqo_set_threads.argtypes = [I]
     L.jqo_init()
     assert L.jqo_sizeof_game() == GAME_DTYPE.itemsize, (L.jqo_sizeof_game(), GAME_DTYPE.itemsize)
     if RECENCY_LUT_PATH.exists():
@@ -428,6 +431,32 @@ def batch_observe(batch: "Batch", g0: int, g1: int) -> tuple[np.ndarray, np.ndar
     gl = np.zeros((g1 - g0, OBS_G), np.float32)
     lib().jqo_batch_observe(_p(batch.games), g0, g1, _p(sp), _p(gl))
     return sp, gl
+
+
+class CpuEnv:
+    """The CPU baseline: n oracle games stepped with jqo_batch_cpu_env_step."""
+
+    CAP = 1024
+
+    def __init__(self, setups: np.ndarray, pool: np.ndarray, *, show_mode: int = 2, max_num_moves: int = 4000):
+        self.batch = Batch(setups, show_mode=show_mode, max_num_moves=max_num_moves)
+        self.n = self.batch.n
+        self.pool = np.ascontiguousarray(pool, dtype=np.int8).reshape(-1, 120)
+        self.ids = np.zeros((self.n, self.CAP), np.int32)
+        self.counts = np.zeros(self.n, np.int32)
+        self.mask = np.zeros((self.n, 2081), np.uint8)
+        self.sp = np.zeros((self.n, OBS_C, 17, 17), np.float32)
+        self.gl = np.zeros((self.n, OBS_G), np.float32)
+        self.step(-1, sampler=0, seed=0, obs=False)
+
+    def step(self, ply: int, *, sampler: int, seed: int, obs: bool = True) -> int:
+        return int(lib().jqo_batch_cpu_env_step(
+            _p(self.batch.games), self.n, _p(self.pool), len(self.pool), sampler, seed, ply, ply, _p(self.ids),
+            self.CAP, _p(self.counts), _p(self.mask), _p(self.sp) if obs else None, _p(self.gl) if obs else None))
+
+
+def set_threads(n: int) -> None:
+    lib().jqo_set_threads(int(n))
 
 
 def omp_threads() -> int:
