@@ -81,7 +81,7 @@ struct ObsLds {
     float dec[32];                   // code -> f32
     uint32_t decb[32];               // code -> bf16 bits
     int8_t cpid[CELL_STRIDE];        // canonical cell -> pid (-1 empty)
-    uint8_t bval[BC_COUNT * 12 + 4]; // belief row code x type -> value code
+    alignas(4) uint8_t bval[BC_COUNT * 12 + 4]; // belief row code x type -> value code
     float turnv[2];
 };
 
@@ -190,7 +190,7 @@ __device__ __forceinline__ void piece_load(const State &S, int env, int obs, int
 // Scatter one pid's nonzero elements into bits / img.
 template <bool EXT = false, bool AUXC = false>
 __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, int m, const PieceIn &P,
-                                              const float rc[4], const uint16_t rk[4], const uint32_t own_types[4],
+                                              const float rc[4], const uint16_t rk[4], const uint32_t otb[4],
                                               ObsLds &L, const float *ext = nullptr, ExtLds *X = nullptr)
 {
     const int tm = (obs + 2) & 3, le = (obs + 1) & 3, team = obs & 1;
@@ -217,9 +217,11 @@ __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, i
             const int bc = P.bcode < BC_COUNT ? P.bcode : 0;
             const int c0 = rel == 1 ? 12 : rel == 2 ? 27 : 39;
             const int base = rel == 1 ? RG0_B : RG1_B, start = rel == 1 ? RG0_S : RG1_S;
-#pragma unroll 1
+            const uint32_t *bw = reinterpret_cast<const uint32_t *>(&L.bval[bc * 12]);   // the 12 codes
+            const uint32_t b3[3] = {bw[0], bw[1], bw[2]};
+#pragma unroll
             for (int j = 0; j < 12; ++j) {
-                const uint8_t v = L.bval[bc * 12 + j];
+                const uint8_t v = (uint8_t)(b3[j >> 2] >> (8 * (j & 3)));
                 if (v) set_code(L, base, start, (c0 + j) * NC + k, m, v);
             }
         }
@@ -255,11 +257,11 @@ __device__ __forceinline__ void piece_scatter(int show_mode, int obs, int pid, i
             for (uint32_t hits = P.kmask; hits; hits &= hits - 1) {
                 const int sl = __builtin_ctz(hits);
                 set_el(L, (223 + sl) * NC + k);
-                const uint32_t tw = sl < 8 ? own_types[0] : sl < 16 ? own_types[1] : sl < 24 ? own_types[2] : own_types[3];
-                const int gt = (tw >> ((sl & 7) * 4)) & 15;   // the killed piece's type
+                const int gt = (int)(((otb[0] >> sl) & 1u) | (((otb[1] >> sl) & 1u) << 1) | (((otb[2] >> sl) & 1u) << 2) |
+                                     (((otb[3] >> sl) & 1u) << 3));   // the killed piece's type
                 if (gt >= 2 && gt <= 13) tcnt += 1ull << (5 * (gt - 2));
             }
-#pragma unroll 1
+#pragma unroll
             for (int q = 0; q < 12; ++q) {
                 const int c = (int)((tcnt >> (5 * q)) & 31u);
                 if (c) set_code(L, RG3_B, RG3_S, (211 + q) * NC + k, m,
@@ -388,13 +390,15 @@ __device__ __forceinline__ int piece_of_thread(int t, int obs)
 }
 
 // One producer thread's inputs of a row (thread roles below), everything that
-// depends only on (env, observer): gathered in one round of independent loads.
+// depends only on (env, observer): gathered in one round of independent vector
+// loads. Nothing here is a scalar load: a kernel that prefetches the next row
+// while it works on LDS would otherwise wait for the prefetch at its next LDS
+// fence (scalar loads and LDS operations share one wait counter).
 struct RowIn {
     PieceIn P;              // t < NP
-    uint32_t own_types[4];  // the observer's 30 piece types, 4 bits each
+    int own_tp;             // lane l < 30 of every wave: type of the observer's piece l (& 15)
+    uint32_t ew;            // lane l < 8 of every wave: word l of the env record
     int hist;               // T_HIST <= t < T_FLAGS: ring slot t - T_HIST as stored
-    int mc, mslc, hmeta;
-    int sdead, sflag, remtrk;
     int rem;                // t < 24: remaining count behind global feature t
 };
 
@@ -403,15 +407,9 @@ struct RowIn {
 // 160..166 the whole-plane seat flags; 0..27 also write the 28 globals.
 __device__ __forceinline__ void row_fetch(const State &S, int env, int obs, int t, RowIn &R)
 {
-    const EnvRec &E = S.env[env];   // uniform: scalar loads
-    R.mc = E.mc; R.mslc = E.mslc; R.hmeta = E.hmeta;
-    R.sdead = E.sdead; R.sflag = E.sflag; R.remtrk = E.remtrk[obs];
-    for (int w = 0; w < 4; ++w) {
-        uint32_t v = 0;
-        for (int j = 0; j < 8 && w * 8 + j < 30; ++j)
-            v |= (uint32_t)(S.piece[pc_idx(env, obs * 30 + w * 8 + j)].ptype & 15) << (4 * j);
-        R.own_types[w] = v;
-    }
+    const int l = t & 63;
+    R.ew = l < 8 ? reinterpret_cast<const uint32_t *>(&S.env[env])[l] : 0u;
+    R.own_tp = l < 30 ? (S.piece[pc_idx(env, obs * 30 + l)].ptype & 15) : 0;
     R.hist = 0;
     R.rem = 0;
     const int pid = t < PID_STRIDE ? piece_of_thread(t, obs) : -1;
@@ -423,6 +421,17 @@ __device__ __forceinline__ void row_fetch(const State &S, int env, int obs, int 
     }
 }
 
+// The observer of `row` (row_obs) as a per-lane vector load: lane 0 holds it,
+// the other lanes read a neighbouring entry so the address is not uniform.
+// Taken with __builtin_amdgcn_readfirstlane where it is used.
+__device__ __forceinline__ int row_obs_prefetch(const State &S, const int8_t *observer, int all_seats, int row,
+                                                int nrows)
+{
+    const int r = min(row + (int)(threadIdx.x & 1), nrows - 1);
+    if (all_seats) return observer ? observer[r] : r;
+    return observer ? observer[r] : S.env[r].turn;
+}
+
 // Fill a cleared buffer with row (env, obs) from the fetched inputs, thread t
 // in [0, 256). Only the recency-table gathers are loads here. No thread reads
 // what another one writes, so no barrier is needed inside.
@@ -431,6 +440,15 @@ template <bool EXT = false, bool AUXC = false>
 __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, const RowIn &R, ObsLds &L,
                                          float *glob_row, const float *ext = nullptr, ExtLds *X = nullptr)
 {
+    // env-record fields and the observer's piece types, from the fetched lanes
+    const int mc = __builtin_amdgcn_readlane((int)R.ew, 2), mslc = __builtin_amdgcn_readlane((int)R.ew, 3);
+    const int hmeta = __builtin_amdgcn_readlane((int)R.ew, 4);
+    const uint32_t w6 = (uint32_t)__builtin_amdgcn_readlane((int)R.ew, 6);
+    const uint32_t w7 = (uint32_t)__builtin_amdgcn_readlane((int)R.ew, 7);
+    const int sdead = w6 & 0xFF, sflag = (w6 >> 8) & 0xFF;
+    const int remtrk = (obs < 2 ? w6 >> (16 + 8 * obs) : w7 >> (8 * (obs - 2))) & 0xFF;
+    uint32_t otb[4];   // bit planes of the observer's 30 piece types
+    for (int b = 0; b < 4; ++b) otb[b] = (uint32_t)__builtin_amdgcn_ballot_w64(((R.own_tp >> b) & 1) != 0);
     const int pid = t < PID_STRIDE ? piece_of_thread(t, obs) : -1;
     if (pid >= 0) {
         float rc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -438,11 +456,11 @@ __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, 
         if ((unsigned)R.P.pos < (unsigned)NC && t >= 64) {   // enemy pieces on the board
             const int last[4] = {R.P.ldir, R.P.ldir, R.P.lchain, R.P.fstep};
             for (int q = 0; q < 4; ++q) {
-                if (AUXC) rk[q] = recency_code(R.mc, last[q]);
-                else rc[q] = recency_at(S, R.mc, last[q], q);
+                if (AUXC) rk[q] = recency_code(mc, last[q]);
+                else rc[q] = recency_at(S, mc, last[q], q);
             }
         }
-        piece_scatter<EXT, AUXC>(S.show_mode, obs, pid, m, R.P, rc, rk, R.own_types, L, ext, X);
+        piece_scatter<EXT, AUXC>(S.show_mode, obs, pid, m, R.P, rc, rk, otb, L, ext, X);
     } else if (t < PID_STRIDE) {   // the 8 spare threads clear the padding pids' recency
         const int pad = NP + (t < 64 ? t - 60 : t - 120);
         for (int q = 0; q < 4; ++q) {
@@ -450,7 +468,7 @@ __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, 
             else L.rec[pad][q] = 0.f;
         }
     } else if (t < T_FLAGS) {   // move_history (129-160), observation.py:1207-1231
-        const int cnt = R.hmeta & 0xFF, head = (R.hmeta >> 8) & 31;
+        const int cnt = hmeta & 0xFF, head = (hmeta >> 8) & 31;
         const int d = (head - 1 - (t - T_HIST)) & 31;   // plane of this ring slot (0 = most recent)
         if (d < cnt) {
             const int e = R.hist;
@@ -461,7 +479,7 @@ __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, 
         }
     } else if (t < T_END) {   // whole planes: dead_flags 51-53, flag_revealed 54-57
         const int j = t - T_FLAGS;
-        const bool on = j < 3 ? ((R.sdead >> seat_rel(obs, j + 1)) & 1) : ((R.sflag >> seat_rel(obs, j - 3)) & 1);
+        const bool on = j < 3 ? ((sdead >> seat_rel(obs, j + 1)) & 1) : ((sflag >> seat_rel(obs, j - 3)) & 1);
         if (on) {
             const int e0 = (51 + j) * NC, e1 = e0 + NC;
             for (int w = e0 >> 5; w <= (e1 - 1) >> 5; ++w) {
@@ -472,17 +490,17 @@ __device__ __forceinline__ void row_fill(const State &S, int obs, int m, int t, 
         }
     }
     if (t == 0) {   // turn_history: float64 divide, then rounded to float32 (observation.py:1000-1021)
-        double dp = (double)R.mslc / 200.0; if (dp > 1.0) dp = 1.0;
-        double mp = (double)R.mc / 4000.0; if (mp > 1.0) mp = 1.0;
+        double dp = (double)mslc / 200.0; if (dp > 1.0) dp = 1.0;
+        double mp = (double)mc / 4000.0; if (mp > 1.0) mp = 1.0;
         L.turnv[0] = (float)dp; L.turnv[1] = (float)mp;
     }
     if (glob_row && t < 28) {   // globals (observation.py:1623-1651)
         float v;
         if (t < 24) {   // remaining counts of the left / right enemy
             const int seat = t < 12 ? (obs + 1) & 3 : (obs + 3) & 3;
-            v = ((R.remtrk >> seat) & 1) ? (float)R.rem : 0.f;
+            v = ((remtrk >> seat) & 1) ? (float)R.rem : 0.f;
         } else {   // flag_revealed of self, teammate, left, right
-            v = (float)((R.sflag >> seat_rel(obs, t - 24)) & 1);
+            v = (float)((sflag >> seat_rel(obs, t - 24)) & 1);
         }
         glob_row[t] = v;
     }
@@ -808,15 +826,20 @@ __global__ __launch_bounds__(OBS_THREADS) __attribute__((amdgpu_waves_per_eu(4, 
     obs_setup(L, t, OBS_THREADS);
     obs_clear(L, t, OBS_THREADS);
     RowIn R;
-    row_fetch(S, row_env(blockIdx.x, all_seats), row_obs(S, observer, all_seats, blockIdx.x), t, R);
+    int ob = row_obs(S, observer, all_seats, blockIdx.x);
+    row_fetch(S, row_env(blockIdx.x, all_seats), ob, t, R);
+    int obp = row_obs_prefetch(S, observer, all_seats, blockIdx.x + G, nrows);   // observer of the next row
     lds_barrier();
     for (int row = blockIdx.x; row < nrows; row += G) {
         uint8_t *rowp = spatial + (size_t)row * OBS_ROW;
         const int m = (int)((uintptr_t)rowp & 15);
-        row_fill<false, true>(S, row_obs(S, observer, all_seats, row), m, t, R, L,
-                              glob ? glob + (size_t)row * 28 : nullptr);
+        row_fill<false, true>(S, ob, m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr);
         lds_barrier();
-        if (row + G < nrows) row_fetch(S, row_env(row + G, all_seats), row_obs(S, observer, all_seats, row + G), t, R);
+        if (row + G < nrows) {
+            ob = __builtin_amdgcn_readfirstlane(obp) & 3;
+            row_fetch(S, row_env(row + G, all_seats), ob, t, R);
+            obp = row_obs_prefetch(S, observer, all_seats, row + 2 * G, nrows);
+        }
         obs_emit_u8(L, rowp, m, aux ? aux + (size_t)row * AUXC_ROW : nullptr, t);
         lds_barrier();
         obs_clear(L, t, OBS_THREADS);
