@@ -59,8 +59,8 @@ def parse():
                     help="fused: jq_env_step; separate: jq_sample_* + jq_step + jq_reset_terminated + jq_legal; "
                          "dropin: GpuRollout's f32 observation, bool mask, canonical step and device reset")
     ap.add_argument("--seed", type=int, default=0x4A51)
-    ap.add_argument("--cpu-envs", type=int, default=2048)
-    ap.add_argument("--cpu-steps", type=int, default=12)
+    ap.add_argument("--cpu-envs", type=int, default=4096)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (counter calibration) and exit")
@@ -92,37 +92,43 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(envs: int, steps: int, sampler: int, obs: bool, seed: int) -> dict:
+def cpu_baseline(envs: int, seconds: float, sampler: int, obs: bool, seed: int) -> dict:
     """The C oracle (a scalar port, OpenMP over games) on this host's cores, on a
     bounded sample of the same workload: sample -> step -> pool restart -> sorted
     legal ids + canonical mask (+ float32 observation of the acting seat), games
-    first played into mixed stages; once on every host thread and once on one."""
+    first played into mixed stages. Timed for at least `seconds` on every host
+    thread (`envs` games), then for at least 0.8 x `seconds` on one thread
+    (envs / 4 games)."""
     import numpy as np
 
     from oracle import oracle as O
 
-    setups = np.stack([O.random_setup(i) for i in range(envs)])
-    env = O.CpuEnv(setups, O.setup_pool(42, 1000))
-    for k in range(64):   # leave the opening: games spread over plies 0-64
-        env.step(k, sampler=sampler, seed=seed, obs=False)
+    pool = O.setup_pool(42, 1000)
     all_threads = O.omp_threads()
 
-    def timed(nsteps: int, k0: int) -> float:
-        env.step(k0, sampler=sampler, seed=seed, obs=obs)   # first touch of the output pages
-        t0 = time.perf_counter()
-        for k in range(nsteps):
-            env.step(k0 + 1 + k, sampler=sampler, seed=seed, obs=obs)
-        return envs * nsteps / (time.perf_counter() - t0)
+    def timed(n: int, target: float) -> tuple[float, int]:
+        env = O.CpuEnv(np.stack([O.random_setup(i) for i in range(n)]), pool)
+        for k in range(64):   # leave the opening: games spread over plies 0-64
+            env.step(k, sampler=sampler, seed=seed, obs=False)
+        env.step(64, sampler=sampler, seed=seed, obs=obs)   # first touch of the output pages
+        t0, k = time.perf_counter(), 0
+        while True:
+            env.step(65 + k, sampler=sampler, seed=seed, obs=obs)
+            k += 1
+            el = time.perf_counter() - t0
+            if el >= target:
+                return n * k / el, k
 
-    v_all = timed(steps, 100)
+    v_all, k_all = timed(envs, seconds)
     O.set_threads(1)
-    v_one = timed(max(1, steps // 4), 200)
+    n_one = max(1, envs // 4)
+    v_one, k_one = timed(n_one, 0.8 * seconds)
     O.set_threads(all_threads)
     work = "step + sorted legal ids + canonical mask" + (" + f32 obs" if obs else "")
     return {"value": round(v_all, 1), "unit": "env-steps/s", "cores": all_threads, "kind": "port",
             "single_core_value": round(v_one, 1), "cpu_model": cpu_model(),
-            "sample": f"{envs} games x {steps} env-steps on {all_threads} threads and {envs} x {max(1, steps // 4)} "
-                      f"on 1 ({work}, {'logits' if sampler else 'uniform'} sampler, HALF_DARK, after 64 untimed steps)"}
+            "sample": f"{envs} games x {k_all} env-steps on {all_threads} threads and {n_one} x {k_one} on 1 "
+                      f"({work}, {'logits' if sampler else 'uniform'} sampler, HALF_DARK, after 64 untimed steps)"}
 
 
 # device kernel that writes the observation rows, per output format
@@ -302,7 +308,7 @@ def main() -> int:
                            "kernel_ms": round(ms_total / K, 4), "bytes_per_launch": round(step_bytes * n)}
     b.close()
     if not args.no_cpu:
-        rec["cpu_baseline"] = cpu_baseline(args.cpu_envs, args.cpu_steps, 1 if sampler == "logits" else 0,
+        rec["cpu_baseline"] = cpu_baseline(args.cpu_envs, args.cpu_seconds, 1 if sampler == "logits" else 0,
                                            with_obs, args.seed)
     print(json.dumps(rec), flush=True)
     return 0

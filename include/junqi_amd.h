@@ -234,7 +234,13 @@ int jq_sample_logits(jq_env *env, const int8_t *acting, const int32_t *counts, c
  * mask are written and JQ_E_CAPACITY comes back before values and the
  * observation). hash: device uint64 (N), each env's Zobrist hash after its ply
  * and before any restart; terminated / reward as jq_step's; actions_out the
- * action taken (world id, -1 none). */
+ * action taken (world id, -1 none).
+ * Sampling reads the rows the previous jq_env_step / jq_legal call wrote into
+ * counts / offsets / values: after jq_reset_seeded, jq_reset_lineups or
+ * jq_reset_terminated those rows describe the old positions, so call jq_legal
+ * (or pass actions) before the next sampled step. A stale id that is not legal
+ * in the new position is rejected like any illegal action (that env does not
+ * move); reads stay inside values_capacity. */
 int jq_env_step(jq_env *env, const int32_t *actions, int32_t sampler, uint64_t sample_seed, uint64_t ply,
                 int64_t reset_seed, int32_t *counts, int32_t *offsets, int32_t *values, int64_t values_capacity,
                 int32_t *mask_words, int32_t obs_fmt, void *spatial, void *aux, float *global,
