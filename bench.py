@@ -132,7 +132,7 @@ def cpu_baseline(envs: int, seconds: float, sampler: int, obs: bool, seed: int) 
 
 
 # device kernel that writes the observation rows, per output format
-OBS_KERNEL = {"f32": "jq::k_observe<0>", "bf16": "jq::k_observe<1>", "u8": "jq::k_observe_u8_persist"}
+OBS_KERNEL = {"f32": "jq::k_observe<0, false>", "bf16": "jq::k_observe<1, false>", "u8": "jq::k_observe_u8_persist"}
 
 
 def measured_traffic(kernel: str, games: int):
