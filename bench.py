@@ -20,6 +20,7 @@ Prints one JSON line. Usage: python bench.py [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -207,16 +208,17 @@ def main() -> int:
     torch.cuda.synchronize(dev)
     plies0 = b.get_field("move_counter")[:, 0]
 
-    def one_step(ply: int, slot: int, ev_obs=None):
+    def one_step(ply: int, slot: int):
         s = torch.cuda.current_stream(dev).cuda_stream
         if args.path == "fused":
-            # sample from the previous CSR rows, ply, restart, next seat's CSR + mask;
-            # the observation is launched on its own so events can time its kernel
+            # one call: sample from the previous CSR rows, ply, restart, next seat's
+            # CSR + mask, observation (the library times the observation kernel)
             L.check(lib.jq_env_step(h, None, smp, args.seed, ply, ply, b.counts.data_ptr(), b.offsets.data_ptr(),
-                                    b.values.data_ptr(), cap, b.mask_words.data_ptr(), fmt_code, None, None, None,
-                                    term[slot].data_ptr(), reward[slot].data_ptr(), hsh[slot].data_ptr(),
+                                    b.values.data_ptr(), cap, b.mask_words.data_ptr(), fmt_code, P(spatial), P(aux),
+                                    P(glob), term[slot].data_ptr(), reward[slot].data_ptr(), hsh[slot].data_ptr(),
                                     acts[slot].data_ptr(), s))
-        elif args.path == "separate":
+            return
+        if args.path == "separate":
             if smp == L.SAMPLE_LOGITS:
                 L.check(lib.jq_sample_logits(h, None, b.counts.data_ptr(), b.offsets.data_ptr(),
                                              b.values.data_ptr(), cap, args.seed, ply, acts[slot].data_ptr(), None, s))
@@ -238,28 +240,26 @@ def main() -> int:
             L.check(lib.jq_legal(h, None, b.counts.data_ptr(), b.offsets.data_ptr(), b.values.data_ptr(), cap,
                                  None, mask_bool.data_ptr(), s))
         if with_obs:
-            if ev_obs is not None:
-                ev_obs[0].record()
             L.check(lib.jq_observe(h, None, fmt_code, 0, spatial.data_ptr(), P(aux), glob.data_ptr(), s))
-            if ev_obs is not None:
-                ev_obs[1].record()
 
     for w in range(args.warmup):
         one_step(stagger + w, K)
     torch.cuda.synchronize(dev)
-    obs_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(K)] if with_obs else [None] * K
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    L.check(lib.jq_obs_timing(h, 1))   # HIP events around each observation launch, on its stream
     torch.cuda.synchronize(dev)
     wall0 = time.perf_counter()
     t_start.record()
     for k in range(K):
-        one_step(stagger + args.warmup + k, k, obs_events[k])
+        one_step(stagger + args.warmup + k, k)
     t_end.record()
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
     ms_total = t_start.elapsed_time(t_end)
-    obs_ms = sum(a.elapsed_time(c) for a, c in obs_events) / K if with_obs else None
+    obs_total, obs_n = ctypes.c_double(0.0), ctypes.c_int64(0)
+    L.check(lib.jq_obs_timing_read(h, ctypes.byref(obs_total), ctypes.byref(obs_n)))
+    L.check(lib.jq_obs_timing(h, 0))
+    obs_ms = obs_total.value / max(1, obs_n.value) if with_obs else None
     kbar = int(b.offsets[-1].item()) / n
     ended = int(term[:K].sum().item())
 

@@ -203,6 +203,15 @@ int jq_observe(jq_env *env, const int8_t *observer, int32_t fmt, int32_t all_sea
 int jq_upload_beliefs(jq_env *env, const void *beliefs, int32_t from_host, void *stream);
 int jq_clear_beliefs(jq_env *env);
 
+/* Kernel timing of the observation (instrumentation; no counterpart in the
+ * reference). jq_obs_timing(env, 1) brackets every following observation
+ * launch of the handle (jq_observe and the observation inside jq_env_step) with
+ * a pair of HIP events on the launch's stream; jq_obs_timing_read waits for the
+ * recorded launches and returns their summed kernel time and count, then starts
+ * a new count. jq_obs_timing(env, 0) stops recording. */
+int jq_obs_timing(jq_env *env, int32_t enable);
+int jq_obs_timing_read(jq_env *env, double *total_ms, int64_t *launches);
+
 /* The 256-entry float32 decode table of JQ_OBS_U8 codes (host pointer out). */
 int jq_obs_decode_table(float *host_out256);
 
@@ -235,6 +244,10 @@ int jq_sample_logits(jq_env *env, const int8_t *acting, const int32_t *counts, c
  * observation). hash: device uint64 (N), each env's Zobrist hash after its ply
  * and before any restart; terminated / reward as jq_step's; actions_out the
  * action taken (world id, -1 none).
+ * With a u8 observation and values_capacity >= N * JQ_MAX_LEGAL the CSR pass
+ * runs on a library-owned side stream beside the observation (they share no
+ * data); `stream` waits for it before the call's work counts as done, so the
+ * call stays ordered on `stream` like any other.
  * Sampling reads the rows the previous jq_env_step / jq_legal call wrote into
  * counts / offsets / values: after jq_reset_seeded, jq_reset_lineups or
  * jq_reset_terminated those rows describe the old positions, so call jq_legal

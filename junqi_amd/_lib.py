@@ -44,7 +44,8 @@ _EXPORTS = [
     "jq_last_error", "jq_version", "jq_create", "jq_destroy", "jq_num_envs", "jq_upload_zobrist",
     "jq_upload_recency", "jq_upload_setup_pool", "jq_reset_lineups", "jq_reset_seeded",
     "jq_generate_lineups", "jq_generate_pool", "jq_generate_styled", "jq_board_tables", "jq_reset_terminated", "jq_step",
-    "jq_legal", "jq_legal_slots", "jq_observe", "jq_obs_decode_table", "jq_sample_uniform", "jq_sample_logits",
+    "jq_legal", "jq_legal_slots", "jq_observe", "jq_obs_timing", "jq_obs_timing_read", "jq_obs_decode_table",
+    "jq_sample_uniform", "jq_sample_logits",
     "jq_env_step", "jq_field_info", "jq_get_field", "jq_set_field", "jq_field_ptr", "jq_finalize_import",
     "jq_finalize_import_masked", "jq_rehash", "jq_validate_lineup",
     "jq_sync", "jq_history_create", "jq_history_destroy", "jq_history_bytes", "jq_history_snapshot",
@@ -92,6 +93,8 @@ def bind(L: C.CDLL) -> C.CDLL:
         "jq_legal_slots": ([P, P, P, P], C.c_int),
         "jq_observe": ([P, P, I32, I32, P, P, P, P], C.c_int),
         "jq_obs_decode_table": ([P], C.c_int),
+        "jq_obs_timing": ([P, I32], C.c_int),
+        "jq_obs_timing_read": ([P, C.POINTER(C.c_double), C.POINTER(I64)], C.c_int),
         "jq_sample_uniform": ([P, P, P, P, I64, U64, U64, P, P], C.c_int),
         "jq_sample_logits": ([P, P, P, P, P, I64, U64, U64, P, P, P], C.c_int),
         "jq_env_step": ([P, P, I32, U64, U64, I64, P, P, P, I64, P, I32, P, P, P, P, P, P, P, P], C.c_int),

@@ -33,6 +33,12 @@ struct jq_env {
     int8_t *pool = nullptr;          // setup pool buffer (reused while uploads fit)
     int32_t pool_cap = 0;            // entries the pool buffer holds
     int32_t *total_host = nullptr;   // pinned host word for CSR totals read back
+    hipStream_t side = nullptr;      // jq_env_step's CSR pass beside the observation
+    hipEvent_t ev_step = nullptr, ev_csr = nullptr;
+    bool obs_timing = false;         // jq_obs_timing: events around every observation launch
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> obs_ev;
+    size_t obs_ev_used = 0;
+    hipEvent_t obs_t_end = nullptr;  // end event of a launch whose begin jq_env_step recorded
 };
 
 // Rollout history: per-step copies of every per-env state block.
@@ -259,6 +265,27 @@ int obs_u8_grid(jq_env *e)
     return JQ_OK;
 }
 
+// With jq_obs_timing on: record the begin event of the next observation launch
+// on `stream` and hand back its end event (else *t_end = nullptr).
+int obs_timing_begin(jq_env *e, void *stream, hipEvent_t *t_end)
+{
+    *t_end = nullptr;
+    if (!e->obs_timing) return JQ_OK;
+    if (e->obs_ev_used == e->obs_ev.size()) {   // a pair per launch, reused after jq_obs_timing_read
+        hipEvent_t a = nullptr, b = nullptr;
+        HIP_TRY(hipEventCreate(&a));
+        if (hipEventCreate(&b) != hipSuccess) {
+            (void)hipEventDestroy(a);
+            return fail(JQ_E_HIP, "hipEventCreate failed");
+        }
+        e->obs_ev.emplace_back(a, b);
+    }
+    const auto &pr = e->obs_ev[e->obs_ev_used++];
+    HIP_TRY(hipEventRecord(pr.first, strm(stream)));
+    *t_end = pr.second;
+    return JQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -311,9 +338,14 @@ int jq_destroy(jq_env *e)
     if (!e) return JQ_OK;
     (void)hipSetDevice(e->device);
 
+    if (e->side) (void)hipStreamSynchronize(e->side);
     for (void *p : e->allocs) (void)hipFree(p);
     if (e->pool) (void)hipFree(e->pool);
     if (e->total_host) (void)hipHostFree(e->total_host);
+    if (e->side) (void)hipStreamDestroy(e->side);
+    if (e->ev_step) (void)hipEventDestroy(e->ev_step);
+    if (e->ev_csr) (void)hipEventDestroy(e->ev_csr);
+    for (auto &pr : e->obs_ev) { (void)hipEventDestroy(pr.first); (void)hipEventDestroy(pr.second); }
     delete e;
     return JQ_OK;
 }
@@ -511,6 +543,10 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
     if (e->ext_on && fmt == JQ_OBS_U8)
         return fail(JQ_E_STATE, "uploaded beliefs are arbitrary floats: observe them as JQ_OBS_F32 or JQ_OBS_BF16");
     const float *x = e->ext_bel;
+    if (fmt == JQ_OBS_U8 && (rc = obs_u8_grid(e)) != 0) return rc;
+    hipEvent_t t_end = e->obs_t_end;   // begin already recorded by jq_env_step
+    e->obs_t_end = nullptr;
+    if (!t_end && (rc = obs_timing_begin(e, stream, &t_end)) != 0) return rc;
     switch (fmt) {
     case JQ_OBS_F32:
         if (e->ext_on)
@@ -525,13 +561,41 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
             hipLaunchKernelGGL((k_observe<1, false>), grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, nullptr);
         break;
     default:
-        if ((rc = obs_u8_grid(e)) != 0) return rc;
         hipLaunchKernelGGL(k_observe_u8_persist, dim3(std::min(nrows, e->obs_blocks)), dim3(OBS_THREADS), 0,
                            strm(stream), e->S, observer, all_seats, static_cast<uint8_t *>(spatial),
                            static_cast<uint8_t *>(aux), global, nrows);
         break;
     }
-    return launch_check("k_observe");
+    if ((rc = launch_check("k_observe")) != 0) return rc;
+    if (t_end) HIP_TRY(hipEventRecord(t_end, strm(stream)));
+    return JQ_OK;
+}
+
+int jq_obs_timing(jq_env *e, int32_t enable)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    e->obs_timing = enable != 0;
+    e->obs_ev_used = 0;
+    return JQ_OK;
+}
+
+int jq_obs_timing_read(jq_env *e, double *total_ms, int64_t *launches)
+{
+    int rc = check_env(e);
+    if (rc) return rc;
+    if (!total_ms || !launches) return fail(JQ_E_ARG, "null output");
+    double sum = 0.0;
+    for (size_t i = 0; i < e->obs_ev_used; ++i) {
+        float ms = 0.f;
+        HIP_TRY(hipEventSynchronize(e->obs_ev[i].second));
+        HIP_TRY(hipEventElapsedTime(&ms, e->obs_ev[i].first, e->obs_ev[i].second));
+        sum += ms;
+    }
+    *total_ms = sum;
+    *launches = (int64_t)e->obs_ev_used;
+    e->obs_ev_used = 0;
+    return JQ_OK;
 }
 
 int jq_upload_beliefs(jq_env *e, const void *beliefs, int32_t from_host, void *stream)
@@ -616,14 +680,42 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
     // next seat's legal sets in one kernel
     hipLaunchKernelGGL(k_env_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, A);
     if ((rc = launch_check("k_env_step")) != 0) return rc;
+    if (spatial && obs_fmt == JQ_OBS_U8 && values_capacity >= (int64_t)e->S.n * JQ_MAX_LEGAL) {
+        // The CSR pass (scan + emit) reads the legal records and writes offsets /
+        // values; the observation reads the state. Neither touches what the other
+        // writes, so the CSR pass runs on a side stream and fills the CUs the
+        // persistent observation grid releases as its blocks finish; the
+        // caller's stream waits for both before anything it enqueues next.
+        if (!e->side) {
+            HIP_TRY(hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking));
+            HIP_TRY(hipEventCreateWithFlags(&e->ev_step, hipEventDisableTiming));
+            HIP_TRY(hipEventCreateWithFlags(&e->ev_csr, hipEventDisableTiming));
+        }
+        // a timing event goes before the release of the side stream, so the
+        // observation's dispatch still follows the step directly
+        if ((rc = obs_timing_begin(e, stream, &e->obs_t_end)) != 0) return rc;
+        HIP_TRY(hipEventRecord(e->ev_step, strm(stream)));
+        HIP_TRY(hipStreamWaitEvent(e->side, e->ev_step, 0));
+        hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, e->side, counts, offsets, e->S.n);
+        if ((rc = launch_check("k_scan")) != 0) return rc;
+        hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, e->side, e->S, offsets, values,
+                           values_capacity);
+        if ((rc = launch_check("k_emit")) != 0) return rc;
+        HIP_TRY(hipEventRecord(e->ev_csr, e->side));
+        rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream);
+        if (e->obs_t_end) {   // the observation failed before its launch: close the timing pair
+            (void)hipEventRecord(e->obs_t_end, strm(stream));
+            e->obs_t_end = nullptr;
+        }
+        HIP_TRY(hipStreamWaitEvent(strm(stream), e->ev_csr, 0));   // joined even if the observation failed
+        return rc;
+    }
     hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, strm(stream), counts, offsets, e->S.n);
     if ((rc = launch_check("k_scan")) != 0) return rc;
     if ((rc = csr_fits(e, offsets, values_capacity, strm(stream))) != 0) return rc;
     hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values,
                        values_capacity);
     if ((rc = launch_check("k_emit")) != 0) return rc;
-    // sequential on purpose: the u8 observation grid holds every CU's LDS, so a
-    // concurrent launch only slows both down
     if (spatial && (rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream)) != 0) return rc;
     return JQ_OK;
 }
