@@ -6,6 +6,7 @@ reference's host-copy API of the device state, the multi-tile CSR scan, and the
 
 from __future__ import annotations
 
+import ctypes
 import hashlib
 import json
 
@@ -127,6 +128,61 @@ def test_csr_capacity(jq):
                                   None, acts.data_ptr(), b.stream))
     assert bool((small == -7).all())
     b.close()
+
+
+def test_env_step_side_stream_csr(jq):
+    """jq_env_step with a u8 observation and a full-size values buffer runs the
+    CSR pass on a side stream beside the observation; with a smaller buffer it
+    runs in line (after the total is read back). Both must give the same rows,
+    masks, observations and step results, on a non-default caller stream whose
+    later work sees the joined results; the observation timing hooks count every
+    launch."""
+    print("[boundary] side-stream CSR pass", flush=True)
+    from junqi_amd import _lib as L
+    n, steps = 3000, 24
+    side, inline = (jq.JunqiBatch(n, show_mode=2, pool_size=64) for _ in range(2))
+    for b in (side, inline):
+        b.reset(31)
+        b.legal()
+    dev = side.device
+    st = torch.cuda.Stream(dev)
+    mk = lambda: (torch.empty((n, 317, 17, 17), dtype=torch.uint8, device=dev),  # noqa: E731
+                  torch.empty((n, L.AUX_BYTES), dtype=torch.uint8, device=dev),
+                  torch.empty((n, 28), dtype=torch.float32, device=dev),
+                  torch.empty(n, dtype=torch.uint8, device=dev), torch.empty(n, dtype=torch.float32, device=dev),
+                  torch.empty(n, dtype=torch.int64, device=dev), torch.empty(n, dtype=torch.int32, device=dev))
+    outs = {"side": mk(), "inline": mk()}
+    caps = {"side": side.values.numel(), "inline": n * 200}
+    assert caps["inline"] < n * L.MAX_LEGAL <= caps["side"]
+    L.check(L.lib.jq_obs_timing(side._h, 1))
+    with torch.cuda.stream(st):
+        for k in range(steps):
+            snap = {}
+            for name, b in (("side", side), ("inline", inline)):
+                sp, aux, gl, te, rw, hs, ac = outs[name]
+                L.check(L.lib.jq_env_step(b._h, None, L.SAMPLE_LOGITS, 5, k, k, b.counts.data_ptr(),
+                                          b.offsets.data_ptr(), b.values.data_ptr(), caps[name],
+                                          b.mask_words.data_ptr(), L.OBS_U8, sp.data_ptr(), aux.data_ptr(),
+                                          gl.data_ptr(), te.data_ptr(), rw.data_ptr(), hs.data_ptr(), ac.data_ptr(),
+                                          st.cuda_stream))
+                # read on the caller's stream right after the call
+                tot = b.offsets[-1].clone()
+                snap[name] = (b.counts.clone(), b.offsets.clone(), b.values[:n * 200].clone(), b.mask_words.clone(),
+                              tot, sp.clone(), aux.clone(), gl.clone(), te.clone(), rw.clone(), hs.clone(), ac.clone())
+            st.synchronize()
+            a, c = snap["side"], snap["inline"]
+            t = int(a[4])
+            assert t == int(c[4]) and t <= n * 200
+            for i, (x, y) in enumerate(zip(a, c)):
+                if i == 2:
+                    x, y = x[:t], y[:t]
+                assert torch.equal(x, y), f"step {k}: output {i} differs"
+    total_ms, launches = ctypes.c_double(), ctypes.c_int64()
+    L.check(L.lib.jq_obs_timing_read(side._h, ctypes.byref(total_ms), ctypes.byref(launches)))
+    L.check(L.lib.jq_obs_timing(side._h, 0))
+    assert launches.value == steps and total_ms.value > 0.0
+    side.close()
+    inline.close()
 
 
 def test_multi_tile_scan(jq):
