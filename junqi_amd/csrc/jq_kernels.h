@@ -639,20 +639,38 @@ struct TurnAfter {
 // One ply of env `env` by its wave (GameState.step_inplace, state.py:700-1167).
 // cell / pos / ptype are the wave's LDS arrays; on return they hold the board
 // after the step (unchanged if the action was not applied).
-__device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t *__restrict__ acting, int act_fmt,
-                         const StepOut &O, int8_t *cell, int16_t *pos, int8_t *ptype, TurnAfter &nx)
-{
-
-    // the board, the piece records, the env record and the action are all
-    // loaded into registers first (one memory round trip), then staged in LDS;
-    // the checks below only decide whether the board is used
+// The board and piece records of one env, lane l's share: the loads of a ply's
+// first memory round trip, which a caller can issue early.
+struct StepLoad {
     int8_t cv[5];
+    PieceRec r0, r1;
+};
+
+__device__ __forceinline__ void step_load(const State &S, int env, int l, StepLoad &P)
+{
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
         const int f = l + 64 * k;
-        cv[k] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : (int8_t)-1;
+        P.cv[k] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : (int8_t)-1;
     }
-    const PieceRec r0 = S.piece[pc_idx(env, l)], r1 = S.piece[pc_idx(env, l + 64)];
+    P.r0 = S.piece[pc_idx(env, l)];
+    P.r1 = S.piece[pc_idx(env, l + 64)];
+}
+
+__device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t *__restrict__ acting, int act_fmt,
+                         const StepOut &O, int8_t *cell, int16_t *pos, int8_t *ptype, TurnAfter &nx,
+                         const StepLoad *pre = nullptr)
+{
+
+    // the board, the piece records, the env record and the action are all
+    // loaded into registers first (one memory round trip, or `pre` issued
+    // earlier by the caller), then staged in LDS; the checks below only decide
+    // whether the board is used
+    StepLoad ld;
+    if (pre) ld = *pre;
+    else step_load(S, env, l, ld);
+    const int8_t *cv = ld.cv;
+    const PieceRec &r0 = ld.r0, &r1 = ld.r1;
     const EnvRec &E = S.env[env];   // uniform: scalar loads
 #pragma unroll
     for (int k = 0; k < 5; ++k)
@@ -1520,6 +1538,8 @@ struct EnvStepArgs {
 // only its own wave (wave_sync), so it never waits on other waves of a block.
 __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, const EnvStepArgs &A, EnvLds &E)
 {
+    StepLoad ld;   // the ply's first loads go out before the sampler's
+    step_load(S, env, l, ld);
     int32_t a;
     if (A.actions) {
         a = A.actions[env];
@@ -1532,7 +1552,7 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
     }
     if (A.actions_out && l == 0) A.actions_out[env] = a;
     TurnAfter nx;
-    step_env(S, env, l, a, nullptr, 0, A.O, E.cell, E.pos, E.ptype, nx);
+    step_env(S, env, l, a, nullptr, 0, A.O, E.cell, E.pos, E.ptype, nx, &ld);
     wave_sync();
     if (A.do_reset && S.pool_size > 0 && nx.term) {
         init_env(S, env, S.pool + (size_t)reset_pool_index(env, A.reset_seed, S.pool_size) * NP, E.cell, E.pos,
