@@ -2,7 +2,7 @@
  * jq_oracle.c -- CPU restatement of the junqi_core rules. TEST INFRASTRUCTURE.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use
- * this file, and only as the checker / the timed CPU baseline. It shares no
+ * this file, and only as the reference answer / the timed CPU baseline. It shares no
  * code with junqi_amd/ (the product).
  *
  * Citations are reference paths (file:line). The restated behaviour is that

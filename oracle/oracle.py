@@ -1,6 +1,6 @@
 """ctypes bindings for the C oracle (test infrastructure only).
 
-The oracle is the checker for the HIP path: only ``tests/``,
+The oracle is what the HIP path is compared with: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
 this module. It loads ``oracle/_build/libjq_oracle.so`` (built by
 ``oracle/build_oracle.py``) and exposes thin numpy-friendly wrappers.

@@ -1,4 +1,4 @@
-"""Pins the C oracle (oracle/jq_oracle.c) before it is trusted as the checker.
+"""Pins the C oracle (oracle/jq_oracle.c) before the HIP path is compared with it.
 
 Each check is chosen so that a plausible mistake fails it: reference golden
 vectors (obs hashes, step scenarios, the recorded 603-ply game), third-party
