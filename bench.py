@@ -132,6 +132,8 @@ def cpu_baseline(envs: int, seconds: float, sampler: int, obs: bool, seed: int) 
                       f"({work}, {'logits' if sampler else 'uniform'} sampler, HALF_DARK, after 64 untimed steps)"}
 
 
+OBS_TIMED_EVERY = 4   # observation launches timed with events: every 4th step of the timed region
+
 # device kernel that writes the observation rows, per output format
 OBS_KERNEL = {"f32": "jq::k_observe<0, false>", "bf16": "jq::k_observe<1, false>", "u8": "jq::k_observe_u8_persist"}
 
@@ -246,11 +248,15 @@ def main() -> int:
         one_step(stagger + w, K)
     torch.cuda.synchronize(dev)
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    L.check(lib.jq_obs_timing(h, 1))   # HIP events around each observation launch, on its stream
+    total0, n0 = ctypes.c_double(0.0), ctypes.c_int64(0)
+    L.check(lib.jq_obs_timing_read(h, ctypes.byref(total0), ctypes.byref(n0)))   # start a new count
     torch.cuda.synchronize(dev)
     wall0 = time.perf_counter()
     t_start.record()
     for k in range(K):
+        # HIP events around the observation launch of every OBS_TIMED_EVERY-th step,
+        # on its stream (each pair costs the step about 6 us of queue time)
+        L.check(lib.jq_obs_timing(h, 1 if k % OBS_TIMED_EVERY == 0 else 0))
         one_step(stagger + args.warmup + k, k)
     t_end.record()
     torch.cuda.synchronize(dev)

@@ -204,11 +204,11 @@ int jq_upload_beliefs(jq_env *env, const void *beliefs, int32_t from_host, void 
 int jq_clear_beliefs(jq_env *env);
 
 /* Kernel timing of the observation (instrumentation; no counterpart in the
- * reference). jq_obs_timing(env, 1) brackets every following observation
- * launch of the handle (jq_observe and the observation inside jq_env_step) with
- * a pair of HIP events on the launch's stream; jq_obs_timing_read waits for the
- * recorded launches and returns their summed kernel time and count, then starts
- * a new count. jq_obs_timing(env, 0) stops recording. */
+ * reference). While jq_obs_timing(env, 1) is in force, every observation launch
+ * of the handle (jq_observe and the observation inside jq_env_step) is
+ * bracketed by a pair of HIP events on the launch's stream; jq_obs_timing(env,
+ * 0) pauses that. jq_obs_timing_read waits for the launches recorded since the
+ * last read and returns their summed kernel time and count. */
 int jq_obs_timing(jq_env *env, int32_t enable);
 int jq_obs_timing_read(jq_env *env, double *total_ms, int64_t *launches);
 

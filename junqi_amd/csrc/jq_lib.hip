@@ -576,7 +576,6 @@ int jq_obs_timing(jq_env *e, int32_t enable)
     int rc = check_env(e);
     if (rc) return rc;
     e->obs_timing = enable != 0;
-    e->obs_ev_used = 0;
     return JQ_OK;
 }
 
