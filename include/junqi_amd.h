@@ -208,7 +208,9 @@ int jq_clear_beliefs(jq_env *env);
  * of the handle (jq_observe and the observation inside jq_env_step) is
  * bracketed by a pair of HIP events on the launch's stream; jq_obs_timing(env,
  * 0) pauses that. jq_obs_timing_read waits for the launches recorded since the
- * last read and returns their summed kernel time and count. */
+ * last read and returns their summed kernel time and count; at most
+ * JQ_OBS_TIMING_MAX launches are recorded between two reads. */
+#define JQ_OBS_TIMING_MAX 65536
 int jq_obs_timing(jq_env *env, int32_t enable);
 int jq_obs_timing_read(jq_env *env, double *total_ms, int64_t *launches);
 

@@ -270,7 +270,7 @@ int obs_u8_grid(jq_env *e)
 int obs_timing_begin(jq_env *e, void *stream, hipEvent_t *t_end)
 {
     *t_end = nullptr;
-    if (!e->obs_timing) return JQ_OK;
+    if (!e->obs_timing || e->obs_ev_used >= JQ_OBS_TIMING_MAX) return JQ_OK;
     if (e->obs_ev_used == e->obs_ev.size()) {   // a pair per launch, reused after jq_obs_timing_read
         hipEvent_t a = nullptr, b = nullptr;
         HIP_TRY(hipEventCreate(&a));
