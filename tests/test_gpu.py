@@ -116,6 +116,14 @@ def test_play_bright_and_dark(jq):
     _play(jq, 24, 160, 1, seed=6, check_every=2, obs_every=2)
 
 
+@pytest.mark.parametrize("show_mode", [0, 1, 2])
+def test_c1_64_games_200_plies(jq, show_mode):
+    # the CPU-reference plumbing configuration: 64 four-player games from seeded
+    # random legal setups, 200 plies of seeded uniform-random legal actions; hash,
+    # state, CSR rows, canonical masks and observations after every ply
+    _play(jq, 64, 200, show_mode, seed=64 + show_mode, check_every=1, obs_every=1)
+
+
 def test_play_move_cap(jq):
     # the env cap (max_num_moves) ends games in a draw after the turn advance
     _play(jq, 16, 90, 2, seed=3, max_moves=60, check_every=3, obs_every=3)
