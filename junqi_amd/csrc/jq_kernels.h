@@ -1281,15 +1281,23 @@ __device__ __forceinline__ int select64(uint64_t x, int k)
 // a bit of that piece's mask, and maps it to a flat cell through an LDS copy of
 // the compact table.
 __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict__ offsets, int32_t *__restrict__ values,
-                                             int64_t cap)
+                                             int64_t cap, int32_t *__restrict__ mask_words)
 {
     const int l = threadIdx.x, h = l >> 5, p = l & 31;
     const int env = 2 * (int)blockIdx.x + h;
     const bool live = env < S.n;
     __shared__ int16_t c2f[NONB + 3];
     __shared__ int32_t start[2][33];   // per half: first id of each piece, start[n] = total
+    // mask_words: the canonical mask of each half's env is built here, in LDS
+    __shared__ uint32_t mbits[2][JQ_MASK_WORDS_PAD];
+    __shared__ uint8_t rot[2][NONB + 3];   // world compact -> canonical compact of the env's acting seat
     for (int c = l; c < NONB; c += 64) c2f[c] = cT.c2f[c];
     const int n = live ? min((int)S.lg[env].n, 30) : 0;
+    if (mask_words) {
+        const int seat = live ? (S.lg[env].seat & 3) : 0;
+        for (int w = p; w < JQ_MASK_WORDS_PAD; w += 32) mbits[h][w] = 0;
+        for (int c = p; c < NONB; c += 32) rot[h][c] = cT.rotc[seat][c];
+    }
     int cnt = 0, src = 0;
     uint64_t m0 = 0, m1 = 0, m2 = 0;
     if (p < n) {
@@ -1314,13 +1322,22 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
             if (j + step < n && start[h][j + step] <= i) j += step;
         const uint64_t w0 = __shfl(m0, j, 32), w1 = __shfl(m1, j, 32), w2 = __shfl(m2, j, 32);
         const int s = __shfl(src, j, 32);
-        if (i < total && (int64_t)base + i < cap) {
+        if (i < total) {
             const int k = i - start[h][j];
             const int c0 = __popcll(w0), c1 = __popcll(w1);
             const int c = k < c0 ? select64(w0, k)
                                  : k < c0 + c1 ? 64 + select64(w1, k - c0) : 128 + select64(w2, k - c0 - c1);
-            values[base + i] = s * NC + c2f[c];
+            if ((int64_t)base + i < cap) values[base + i] = s * NC + c2f[c];
+            if (mask_words) {   // canonical bit (rotated source) * 129 + (rotated destination)
+                const int bit = rot[h][flat_rank(cT.onm, s)] * NONB + rot[h][c];
+                atomicOr(&mbits[h][bit >> 5], 1u << (bit & 31));
+            }
         }
+    }
+    if (mask_words) {
+        __syncthreads();
+        if (live)
+            for (int w = p; w < JQ_MASK_WORDS; w += 32) mask_words[(size_t)env * JQ_MASK_WORDS + w] = (int32_t)mbits[h][w];
     }
 }
 
@@ -1561,9 +1578,10 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
     }
     const int seat = nx.turn;
     const bool off = nx.term || seat < 0 || seat > 3 || ((nx.sdead >> (seat & 3)) & 1);
-    for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) E.bits[w] = 0;
-    if (A.mask_words)
+    if (A.mask_words) {
+        for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) E.bits[w] = 0;
         for (int c = l; c < NONB; c += 64) E.rotl[c] = cT.rotc[seat & 3][c];
+    }
     wave_sync();
     legal_body(S, env, l, seat, off, E.cell, E.bits, E.rotl, E.pos, E.ptype, E.lscr, A.counts, A.mask_words,
                nullptr);

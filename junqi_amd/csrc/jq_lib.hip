@@ -507,7 +507,7 @@ int jq_legal(jq_env *e, const int8_t *acting, int32_t *counts, int32_t *offsets,
     if (values) {
         if ((rc = csr_fits(e, offsets, values_capacity, strm(stream))) != 0) return rc;
         hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values,
-                           values_capacity);
+                           values_capacity, nullptr);
         if ((rc = launch_check("k_emit")) != 0) return rc;
     }
     return JQ_OK;
@@ -674,17 +674,22 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
     A.actions = actions; A.sampler = sampler; A.sample_seed = sample_seed; A.ply = ply; A.offsets = offsets;
     A.values = values; A.values_cap = values_capacity;
     A.actions_out = actions_out; A.O.term = terminated; A.O.reward = reward; A.O.hash = hash;
-    A.do_reset = e->S.pool ? 1 : 0; A.reset_seed = reset_seed; A.counts = counts; A.mask_words = mask_words;
+    A.do_reset = e->S.pool ? 1 : 0; A.reset_seed = reset_seed; A.counts = counts;
+    // The overlapped form moves the CSR pass, and the canonical mask with it,
+    // beside the observation (below); the step kernel then skips the mask.
+    const bool overlap = spatial && obs_fmt == JQ_OBS_U8 && values_capacity >= (int64_t)e->S.n * JQ_MAX_LEGAL;
+    A.mask_words = overlap ? nullptr : mask_words;
     // sample (unless actions are given), ply, restart from the pool and the
     // next seat's legal sets in one kernel
     hipLaunchKernelGGL(k_env_step, dim3(e->S.n), dim3(64), 0, strm(stream), e->S, A);
     if ((rc = launch_check("k_env_step")) != 0) return rc;
-    if (spatial && obs_fmt == JQ_OBS_U8 && values_capacity >= (int64_t)e->S.n * JQ_MAX_LEGAL) {
-        // The CSR pass (scan + emit) reads the legal records and writes offsets /
-        // values; the observation reads the state. Neither touches what the other
-        // writes, so the CSR pass runs on a side stream and fills the CUs the
-        // persistent observation grid releases as its blocks finish; the
-        // caller's stream waits for both before anything it enqueues next.
+    if (overlap) {
+        // The CSR pass (scan + emit, which also builds the canonical mask) reads
+        // the legal records and writes offsets / values / mask words; the
+        // observation reads the state. Neither touches what the other writes, so
+        // the CSR pass runs on a side stream and fills the CUs the persistent
+        // observation grid releases as its blocks finish; the caller's stream
+        // waits for both before anything it enqueues next.
         if (!e->side) {
             HIP_TRY(hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking));
             HIP_TRY(hipEventCreateWithFlags(&e->ev_step, hipEventDisableTiming));
@@ -698,7 +703,7 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
         hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, e->side, counts, offsets, e->S.n);
         if ((rc = launch_check("k_scan")) != 0) return rc;
         hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, e->side, e->S, offsets, values,
-                           values_capacity);
+                           values_capacity, mask_words);
         if ((rc = launch_check("k_emit")) != 0) return rc;
         HIP_TRY(hipEventRecord(e->ev_csr, e->side));
         rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream);
@@ -713,7 +718,7 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
     if ((rc = launch_check("k_scan")) != 0) return rc;
     if ((rc = csr_fits(e, offsets, values_capacity, strm(stream))) != 0) return rc;
     hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, strm(stream), e->S, offsets, values,
-                       values_capacity);
+                       values_capacity, nullptr);
     if ((rc = launch_check("k_emit")) != 0) return rc;
     if (spatial && (rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream)) != 0) return rc;
     return JQ_OK;
