@@ -246,10 +246,11 @@ int jq_sample_logits(jq_env *env, const int8_t *acting, const int32_t *counts, c
  * observation). hash: device uint64 (N), each env's Zobrist hash after its ply
  * and before any restart; terminated / reward as jq_step's; actions_out the
  * action taken (world id, -1 none).
- * With a u8 observation and values_capacity >= N * JQ_MAX_LEGAL the CSR pass
- * runs on a library-owned side stream beside the observation (they share no
- * data); `stream` waits for it before the call's work counts as done, so the
- * call stays ordered on `stream` like any other.
+ * With a u8 observation and values_capacity >= N * JQ_MAX_LEGAL the CSR pass,
+ * which then also writes the canonical mask words, runs on a library-owned
+ * side stream beside the observation (they share no data); `stream` waits for
+ * it before the call's work counts as done, so the call stays ordered on
+ * `stream` like any other.
  * Sampling reads the rows the previous jq_env_step / jq_legal call wrote into
  * counts / offsets / values: after jq_reset_seeded, jq_reset_lineups or
  * jq_reset_terminated those rows describe the old positions, so call jq_legal
