@@ -265,6 +265,22 @@ int obs_u8_grid(jq_env *e)
     return JQ_OK;
 }
 
+// The checks of an observation request (format, buffers, tables it needs).
+int obs_args(const jq_env *e, int32_t fmt, const void *spatial, const void *aux, const float *global)
+{
+    if (!spatial) return fail(JQ_E_ARG, "null spatial output");
+    if (fmt < JQ_OBS_F32 || fmt > JQ_OBS_U8) return fail(JQ_E_ARG, "bad observation format %d", fmt);
+    const int es = fmt == JQ_OBS_F32 ? 4 : fmt == JQ_OBS_BF16 ? 2 : 1;
+    if ((uintptr_t)spatial % es || (global && (uintptr_t)global % 4))
+        return fail(JQ_E_ARG, "observation buffers must be aligned to their element size");
+    if (aux && fmt != JQ_OBS_U8) return fail(JQ_E_ARG, "aux rows belong to the u8 format only");
+    if (aux && (uintptr_t)aux % 16) return fail(JQ_E_ARG, "u8 aux rows must be 16-byte aligned");
+    if ((fmt != JQ_OBS_U8 || aux) && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
+    if (e->ext_on && fmt == JQ_OBS_U8)
+        return fail(JQ_E_STATE, "uploaded beliefs are arbitrary floats: observe them as JQ_OBS_F32 or JQ_OBS_BF16");
+    return JQ_OK;
+}
+
 // With jq_obs_timing on: record the begin event of the next observation launch
 // on `stream` and hand back its end event (else *t_end = nullptr).
 int obs_timing_begin(jq_env *e, void *stream, hipEvent_t *t_end)
@@ -337,8 +353,9 @@ int jq_destroy(jq_env *e)
 {
     if (!e) return JQ_OK;
     (void)hipSetDevice(e->device);
-
-    if (e->side) (void)hipStreamSynchronize(e->side);
+    // kernels of any stream, the side stream's included, may still use the
+    // handle's buffers
+    (void)hipDeviceSynchronize();
     for (void *p : e->allocs) (void)hipFree(p);
     if (e->pool) (void)hipFree(e->pool);
     if (e->total_host) (void)hipHostFree(e->total_host);
@@ -530,18 +547,9 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
 {
     int rc = check_env(e);
     if (rc) return rc;
-    if (!spatial) return fail(JQ_E_ARG, "null spatial output");
-    if (fmt < JQ_OBS_F32 || fmt > JQ_OBS_U8) return fail(JQ_E_ARG, "bad observation format %d", fmt);
-    const int es = fmt == JQ_OBS_F32 ? 4 : fmt == JQ_OBS_BF16 ? 2 : 1;
-    if ((uintptr_t)spatial % es || (global && (uintptr_t)global % 4))
-        return fail(JQ_E_ARG, "observation buffers must be aligned to their element size");
-    if (aux && fmt != JQ_OBS_U8) return fail(JQ_E_ARG, "aux rows belong to the u8 format only");
-    if (aux && (uintptr_t)aux % 16) return fail(JQ_E_ARG, "u8 aux rows must be 16-byte aligned");
-    if ((fmt != JQ_OBS_U8 || aux) && !e->rlut_ready) return fail(JQ_E_STATE, "recency table not uploaded");
+    if ((rc = obs_args(e, fmt, spatial, aux, global)) != 0) return rc;
     const int nrows = all_seats ? e->S.n * 4 : e->S.n;
     const dim3 grid(nrows), block(OBS_THREADS);
-    if (e->ext_on && fmt == JQ_OBS_U8)
-        return fail(JQ_E_STATE, "uploaded beliefs are arbitrary floats: observe them as JQ_OBS_F32 or JQ_OBS_BF16");
     const float *x = e->ext_bel;
     if (fmt == JQ_OBS_U8 && (rc = obs_u8_grid(e)) != 0) return rc;
     hipEvent_t t_end = e->obs_t_end;   // begin already recorded by jq_env_step
@@ -668,8 +676,8 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
     if (values_capacity < 0) return fail(JQ_E_ARG, "negative values capacity");
     if (sampler != JQ_SAMPLE_UNIFORM && sampler != JQ_SAMPLE_LOGITS) return fail(JQ_E_ARG, "bad sampler %d", sampler);
     if (!e->zob_ready) return fail(JQ_E_STATE, "upload the Zobrist tables before stepping");
-    if (spatial && (obs_fmt < JQ_OBS_F32 || obs_fmt > JQ_OBS_U8))
-        return fail(JQ_E_ARG, "bad observation format %d", obs_fmt);
+    // the observation's arguments are checked before anything is launched
+    if (spatial && (rc = obs_args(e, obs_fmt, spatial, aux, global)) != 0) return rc;
     EnvStepArgs A = {};
     A.actions = actions; A.sampler = sampler; A.sample_seed = sample_seed; A.ply = ply; A.offsets = offsets;
     A.values = values; A.values_cap = values_capacity;

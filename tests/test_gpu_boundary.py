@@ -130,6 +130,40 @@ def test_csr_capacity(jq):
     b.close()
 
 
+def test_env_step_rejects_bad_observation_buffers_before_stepping(jq):
+    """jq_env_step checks its observation arguments (alignment, format, tables)
+    before it launches anything: a rejected call leaves the state, the CSR and
+    the outputs as they were."""
+    print("[boundary] env_step argument checks", flush=True)
+    from junqi_amd import _lib as L
+    n = 64
+    b = jq.JunqiBatch(n, show_mode=2, pool_size=16)
+    b.reset(12)
+    b.legal()
+    dev = b.device
+    z0, c0, o0 = b.get_field("zobrist").copy(), b.counts.clone(), b.offsets.clone()
+    sp = torch.empty((n, 317, 17, 17), dtype=torch.uint8, device=dev)
+    aux = torch.empty(n * L.AUX_BYTES + 16, dtype=torch.uint8, device=dev)
+    gl = torch.empty(n * 28 + 1, dtype=torch.float32, device=dev)
+    bf = torch.empty(n * 317 * 289 + 1, dtype=torch.int16, device=dev)
+    acts = torch.full((n,), -5, dtype=torch.int32, device=dev)
+    bad = [  # (fmt, spatial, aux, global): misaligned aux, misaligned bf16 rows, unknown format
+        (L.OBS_U8, sp.data_ptr(), aux.data_ptr() + 4, gl.data_ptr()),
+        (L.OBS_BF16, bf.data_ptr() + 1, None, gl.data_ptr()),
+        (7, sp.data_ptr(), None, None),
+    ]
+    for fmt, s_ptr, a_ptr, g_ptr in bad:
+        rc = L.lib.jq_env_step(b._h, None, L.SAMPLE_LOGITS, 1, 0, 0, b.counts.data_ptr(), b.offsets.data_ptr(),
+                               b.values.data_ptr(), b.values.numel(), b.mask_words.data_ptr(), fmt, s_ptr, a_ptr,
+                               g_ptr, None, None, None, acts.data_ptr(), b.stream)
+        torch.cuda.synchronize()
+        assert rc == L.JQ_E_ARG, (fmt, rc)
+        assert np.array_equal(b.get_field("zobrist"), z0), "a rejected call stepped the games"
+        assert torch.equal(b.counts, c0) and torch.equal(b.offsets, o0)
+        assert bool((acts == -5).all()), "a rejected call sampled actions"
+    b.close()
+
+
 def test_env_step_side_stream_csr(jq):
     """jq_env_step with a u8 observation and a full-size values buffer runs the
     CSR pass on a side stream beside the observation; with a smaller buffer it
