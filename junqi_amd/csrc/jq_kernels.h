@@ -414,11 +414,16 @@ __device__ __forceinline__ bool seat_has_move(const int8_t *cell, const int16_t 
         const int pid = seat * 30 + l;
         src = pos[pid];
         const int t = ptype[pid];
-        mov = src >= 0 && t != T_JUNQI && t != T_DILEI && !is_sh(src);
-        if (mov) {
-            eng = t == T_GONGB;
-            for (int k = 0; k < 4; ++k) { const int nb = cT.adj[src][k]; quick |= nb >= 0 && cell[nb] < 0; }
-        }
+        // one round of independent table loads (flags and the four road
+        // neighbours), then the LDS reads: no load waits on another
+        const int s = src >= 0 ? src : 0;
+        const uint16_t fl = cT.cflags[s];
+        const int n0 = cT.adj[s][0], n1 = cT.adj[s][1], n2 = cT.adj[s][2], n3 = cT.adj[s][3];
+        mov = src >= 0 && t != T_JUNQI && t != T_DILEI && !(fl & CF_SH);
+        eng = t == T_GONGB;
+        const bool e0 = (n0 >= 0) & (cell[n0 >= 0 ? n0 : 0] < 0), e1 = (n1 >= 0) & (cell[n1 >= 0 ? n1 : 0] < 0);
+        const bool e2 = (n2 >= 0) & (cell[n2 >= 0 ? n2 : 0] < 0), e3 = (n3 >= 0) & (cell[n3 >= 0 ? n3 : 0] < 0);
+        quick = mov & (e0 | e1 | e2 | e3);
     }
     if (__ballot(mov && quick)) return true;
     uint64_t m0 = 0, m1 = 0, m2 = 0;
@@ -473,6 +478,28 @@ struct StepOut {
     uint8_t *fcap; uint8_t *died; float *reward; int32_t *world;
     uint64_t *hash;   // Zobrist hash after the ply (unchanged when none was applied)
 };
+
+// The values a ply reports (wave-uniform). The caller stores them once its
+// own loads are issued: a load issued after a store waits for that store too.
+struct StepRes {
+    int valid, event, term, winner, draw, fcap, died, world;
+    float reward;
+    uint64_t hash;
+};
+
+__device__ __forceinline__ void write_step_res(const StepOut &O, int env, const StepRes &r)
+{
+    if (O.valid) O.valid[env] = (uint8_t)r.valid;
+    if (O.event) O.event[env] = (int8_t)r.event;
+    if (O.term) O.term[env] = (uint8_t)r.term;
+    if (O.winner) O.winner[env] = (int8_t)r.winner;
+    if (O.draw) O.draw[env] = (uint8_t)r.draw;
+    if (O.fcap) O.fcap[env] = (uint8_t)r.fcap;
+    if (O.died) O.died[env] = (uint8_t)r.died;
+    if (O.reward) O.reward[env] = r.reward;
+    if (O.world) O.world[env] = r.world;
+    if (O.hash) O.hash[env] = r.hash;
+}
 
 // Kill pid at its current cell (state.py:1027-1049). Uniform; lane 0 stores.
 __device__ void kill_piece(const State &S, int env, int8_t *cell, int16_t *pos, const int8_t *ptype, int pid,
@@ -658,7 +685,7 @@ __device__ __forceinline__ void step_load(const State &S, int env, int l, StepLo
 }
 
 __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t *__restrict__ acting, int act_fmt,
-                         const StepOut &O, int8_t *cell, int16_t *pos, int8_t *ptype, TurnAfter &nx,
+                         StepRes &res, int8_t *cell, int16_t *pos, int8_t *ptype, TurnAfter &nx,
                          const StepLoad *pre = nullptr)
 {
 
@@ -680,18 +707,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     const bool was_term = E.term != 0;
     const int seat = E.turn;
     nx.turn = seat; nx.term = was_term; nx.sdead = E.sdead;
-    if (l == 0) {
-        if (O.valid) O.valid[env] = 0;
-        if (O.event) O.event[env] = 0;
-        if (O.term) O.term[env] = was_term;
-        if (O.winner) O.winner[env] = E.winner;
-        if (O.draw) O.draw[env] = E.draw;
-        if (O.fcap) O.fcap[env] = 0;
-        if (O.died) O.died[env] = 0;
-        if (O.reward) O.reward[env] = 0.f;
-        if (O.world) O.world[env] = -1;
-        if (O.hash) O.hash[env] = E.zob;
-    }
+    res = {0, 0, was_term ? 1 : 0, (int)E.winner, (int)E.draw, 0, 0, -1, 0.f, E.zob};
     if (was_term) return;
 
     int src = -1, dst = -1;
@@ -704,7 +720,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     } else if (a >= 0 && a < NC * NC) {
         src = a / NC; dst = a % NC;
     }
-    if (l == 0 && O.world && src >= 0) O.world[env] = src * NC + dst;
+    if (src >= 0) res.world = src * NC + dst;
     if (src < 0) return;
     if (acting && acting[env] != seat) return;
     const uint8_t sdead0 = E.sdead;
@@ -817,16 +833,10 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
         W.hmeta = (hcnt < 32 ? hcnt + 1 : 32) | (((hhead + 1) & 31) << 8);
         W.turn = (int8_t)nturn; W.term = (uint8_t)term; W.winner = (int8_t)win; W.draw = (uint8_t)drw;
         W.sdead = sdead; W.sflag = sflag;
-        if (O.valid) O.valid[env] = 1;
-        if (O.event) O.event[env] = (int8_t)ev;
-        if (O.term) O.term[env] = (uint8_t)term;
-        if (O.winner) O.winner[env] = (int8_t)win;
-        if (O.draw) O.draw[env] = (uint8_t)drw;
-        if (O.fcap) O.fcap[env] = fcap;
-        if (O.died) O.died[env] = (uint8_t)died;
-        if (O.reward) O.reward[env] = (term && !drw && win >= 0) ? (((seat & 1) == win) ? 1.f : -1.f) : 0.f;
-        if (O.hash) O.hash[env] = zob;
     }
+    res.valid = 1; res.event = ev; res.term = term; res.winner = win; res.draw = drw; res.fcap = fcap;
+    res.died = died; res.hash = zob;
+    res.reward = (term && !drw && win >= 0) ? (((seat & 1) == win) ? 1.f : -1.f) : 0.f;
 }
 
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_step(State S, const int32_t *__restrict__ actions,
@@ -838,7 +848,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     __shared__ int16_t pos[PID_STRIDE];
     __shared__ int8_t ptype[PID_STRIDE];
     TurnAfter nx;
-    step_env(S, env, l, actions[env], acting, act_fmt, O, cell, pos, ptype, nx);
+    StepRes res;
+    step_env(S, env, l, actions[env], acting, act_fmt, res, cell, pos, ptype, nx);
+    if (l == 0) write_step_res(O, env, res);
 }
 
 // ------------------------------------------------------------------ reset
@@ -1533,6 +1545,7 @@ __global__ __launch_bounds__(64) void k_sample_logits(State S, const int8_t *__r
 // legal_body work on.
 struct EnvLds {
     alignas(16) uint32_t bits[JQ_MASK_WORDS_PAD];
+    StepRes res;   // the step's reports, parked here across the legal pass
     uint64_t lscr[LSCR_WORDS];
     int16_t pos[PID_STRIDE];
     int8_t ptype[PID_STRIDE];
@@ -1569,7 +1582,11 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
     }
     if (A.actions_out && l == 0) A.actions_out[env] = a;
     TurnAfter nx;
-    step_env(S, env, l, a, nullptr, 0, A.O, E.cell, E.pos, E.ptype, nx, &ld);
+    {
+        StepRes res;
+        step_env(S, env, l, a, nullptr, 0, res, E.cell, E.pos, E.ptype, nx, &ld);
+        if (l == 0) E.res = res;
+    }
     wave_sync();
     if (A.do_reset && S.pool_size > 0 && nx.term) {
         init_env(S, env, S.pool + (size_t)reset_pool_index(env, A.reset_seed, S.pool_size) * NP, E.cell, E.pos,
@@ -1585,6 +1602,7 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
     wave_sync();
     legal_body(S, env, l, seat, off, E.cell, E.bits, E.rotl, E.pos, E.ptype, E.lscr, A.counts, A.mask_words,
                nullptr);
+    if (l == 0) write_step_res(A.O, env, E.res);   // the step's reports go out last
 }
 
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7, 8))) void k_env_step(State S, EnvStepArgs A)
