@@ -505,9 +505,9 @@ __device__ __forceinline__ void write_step_res(const StepOut &O, int env, const 
 __device__ void kill_piece(const State &S, int env, int8_t *cell, int16_t *pos, const int8_t *ptype, int pid,
                            int reason, int loc, int step, uint64_t &zob)
 {
-    const int cur = pos[pid];
+    const int cur = __builtin_amdgcn_readfirstlane(pos[pid]);
     if ((unsigned)cur >= (unsigned)NC) return;
-    zob ^= zp(S.ztab, pid, ptype[pid], cur);
+    zob ^= zp(S.ztab, pid, __builtin_amdgcn_readfirstlane(ptype[pid]), cur);
     wave_sync();
     if (lane_id() == 0) {
         cell[cur] = -1; pos[pid] = -1;
@@ -521,7 +521,7 @@ __device__ void kill_piece(const State &S, int env, int8_t *cell, int16_t *pos, 
 __device__ void move_piece(const State &S, int env, int8_t *cell, int16_t *pos, const int8_t *ptype, int pid,
                            int src, int dst, uint64_t &zob)
 {   // state.py:1005-1025
-    const int t = ptype[pid];
+    const int t = __builtin_amdgcn_readfirstlane(ptype[pid]);
     zob ^= zp(S.ztab, pid, t, src) ^ zp(S.ztab, pid, t, dst);
     wave_sync();
     if (lane_id() == 0) {
@@ -710,6 +710,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     res = {0, 0, was_term ? 1 : 0, (int)E.winner, (int)E.draw, 0, 0, -1, 0.f, E.zob};
     if (was_term) return;
 
+    a = __builtin_amdgcn_readfirstlane(a);   // wave-uniform: the ply's scalar work stays on the SALU
     int src = -1, dst = -1;
     if (act_fmt == 1) {
         const int as = acting ? acting[env] : seat;
@@ -735,8 +736,8 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     const int step = mc0 + 1;
     int died = 0;
     uint8_t sdead = sdead0, sflag = E.sflag;
-    const int sp = cell[src], dp = cell[dst];
-    const int st = ptype[sp], dt = dp >= 0 ? ptype[dp] : -1;
+    const int sp = __builtin_amdgcn_readfirstlane(cell[src]), dp = __builtin_amdgcn_readfirstlane(cell[dst]);
+    const int st = __builtin_amdgcn_readfirstlane(ptype[sp]), dt = dp >= 0 ? __builtin_amdgcn_readfirstlane(ptype[dp]) : -1;
     const int ss = sp / 30, ds = dp >= 0 ? dp / 30 : -1;
 
     if (st == T_GONGB && engineer_only(cell, src, dst)) {
