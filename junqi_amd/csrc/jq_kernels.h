@@ -348,7 +348,7 @@ __device__ __forceinline__ bool run_clear(const int8_t *cell, int src, int dst, 
         for (int i = 0; i < len; ++i) {
             const int nb = curve ? cT.crays[r][k][i] : cT.rays[r][k][i];
             if (nb == dst) return true;
-            if (cell[nb] >= 0) break;
+            if (__builtin_amdgcn_readfirstlane(cell[nb]) >= 0) break;
         }
     }
     return false;
@@ -369,12 +369,13 @@ __device__ __forceinline__ bool legal_pair(const int8_t *cell, const int8_t *pty
 {
     if (src < 0 || src >= NC || dst < 0 || dst >= NC || src == dst) return false;
     if (!is_on(src) || !is_on(dst)) return false;
-    const int p = cell[src];
+    const int p = __builtin_amdgcn_readfirstlane(cell[src]);   // LDS reads at uniform cells: uniform values
     if (p < 0 || p / 30 != seat) return false;
-    const int t = ptype[p];
+    const int t = __builtin_amdgcn_readfirstlane(ptype[p]);
     if (t < T_ZHADAN || t > T_GONGB) return false;   // JUNQI / DILEI never move (no other value is a piece)
     if (is_sh(src)) return false;
-    if (!landable(cell, dst, seat & 1)) return false;
+    const int q = __builtin_amdgcn_readfirstlane(cell[dst]);   // landable: empty, or an enemy outside a camp
+    if (q >= 0 && (team_of(q) == (seat & 1) || is_camp(dst))) return false;
     const int sx = src % 17, sy = src / 17, dx = dst % 17, dy = dst / 17;
     const int adx = abs(sx - dx), ady = abs(sy - dy);
     if (adx <= 1 && ady <= 1) {
@@ -1066,7 +1067,7 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
     // lanes p and p + 32 share piece p (p < 30), one half of its moves each
     const int h = l >> 5, p = l & 31;
     bool mov = false, eng = false;
-    int src = -1, ridx = -1;
+    int src = -1, ridx = -1, sc = 0;
     uint64_t m0 = 0, m1 = 0, m2 = 0;
     if (!off && p < 30) {
         const int pid = seat * 30 + p;
@@ -1079,11 +1080,15 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
             src = r.pos;
             t = r.ptype;
         }
-        mov = (unsigned)src < (unsigned)NC && t != T_JUNQI && t != T_DILEI && !flat_has(cT.shm, src);
+        // the source cell's flags, compact index and rail index: one round of
+        // independent table loads
+        const int f = (unsigned)src < (unsigned)NC ? src : 0;
+        const int fl = cT.cflags[f], fc = cT.f2c[f], fr = cT.railidx[f];
+        mov = (unsigned)src < (unsigned)NC && t != T_JUNQI && t != T_DILEI && !(fl & CF_SH);
         if (mov) {
             eng = t == T_GONGB;
-            const int sc = flat_rank(cT.onm, src);
-            ridx = flat_has(cT.railm, src) ? flat_rank(cT.railm, src) : -1;
+            sc = fc;
+            ridx = fr;
             const BB m = piece_moves_half(sc, ridx, eng, h, occ, ea);
             m0 = m.w0; m1 = m.w1; m2 = m.w2;
         }
@@ -1114,7 +1119,6 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
     const int cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
     // rank of this piece's source cell among the movable pieces: the movable
     // sources below it in a 129-bit set (compact order is flat order)
-    const int sc = mov ? flat_rank(cT.onm, src) : 0;
     if (lead) atomicOr(reinterpret_cast<unsigned long long *>(&srcset[sc >> 6]), 1ull << (sc & 63));
     wave_sync();
     int rank = 0;
