@@ -243,12 +243,16 @@ __device__ __forceinline__ BB piece_moves_half(int sc, int r, bool engineer, int
         }
     }
     const uint4 q = *reinterpret_cast<const uint4 *>(cT.crayc[r][h]);
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    uint64_t qlo = ((uint64_t)q.y << 32) | q.x, qhi = ((uint64_t)q.w << 32) | q.z;   // cells in walk order
     bool open = true;
-#pragma unroll
-    for (int i = 0; i < 12; ++i) {
-        const int c = (int)((qw[i >> 2] >> (8 * (i & 3))) & 0xFF);
-        if (!open || c == 0xFF) { open = false; continue; }
+    // walk until every lane of the wave has met its run's end or first
+    // occupied cell (runs are short and usually blocked early)
+    for (int i = 0; i < 12 && __ballot(open) != 0; ++i) {
+        const int c = (int)(qlo & 0xFF);
+        qlo = (qlo >> 8) | (qhi << 56);
+        qhi >>= 8;
+        if (!open) continue;
+        if (c == 0xFF) { open = false; continue; }
         if (!bb_has(occ, c)) { setbit3(m.w0, m.w1, m.w2, c); continue; }
         if (bb_has(ea, c)) setbit3(m.w0, m.w1, m.w2, c);
         open = false;
@@ -587,9 +591,11 @@ __device__ __forceinline__ void cm_apply(const State &S, int env, bool is_eat, i
     // v6 reverse projection: observer's own pids V had eaten (directly or by chain),
     // plus V itself when V belongs to the observer, are now eaten by K too.
     {
-        uint64_t mlo = 0, mhi = 0;
+        // pids 30o .. 30o + 29 as a 128-bit set (o = 0..3: bit offsets 0, 30, 60, 90)
+        constexpr uint64_t SEAT30 = 0x3FFFFFFFull;
         const int b0 = o * 30;
-        for (int s = 0; s < 30; ++s) { const int gp = b0 + s; if (gp < 64) mlo |= 1ull << gp; else mhi |= 1ull << (gp - 64); }
+        const uint64_t mlo = b0 < 64 ? SEAT30 << b0 : 0ull;
+        const uint64_t mhi = b0 == 0 ? 0ull : b0 < 64 ? SEAT30 >> (64 - b0) : SEAT30 << (b0 - 64);
         uint64_t vlo = (v.dlo | v.clo) & mlo, vhi = (v.dhi | v.chi) & mhi;
         if (Vs == o) { if (V < 64) vlo |= 1ull << V; else vhi |= 1ull << (V - 64); }
         const uint64_t klo = K < 64 ? (1ull << K) : 0ull, khi = K >= 64 ? (1ull << (K - 64)) : 0ull;
