@@ -1316,18 +1316,19 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
     __shared__ uint8_t rot[2][NONB + 3];   // world compact -> canonical compact of the env's acting seat
     for (int c = l; c < NONB; c += 64) c2f[c] = cT.c2f[c];
     const int n = live ? min((int)S.lg[env].n, 30) : 0;
+    const int seat = live ? (S.lg[env].seat & 3) : 0;
     if (mask_words) {
-        const int seat = live ? (S.lg[env].seat & 3) : 0;
         for (int w = p; w < JQ_MASK_WORDS_PAD; w += 32) mbits[h][w] = 0;
         for (int c = p; c < NONB; c += 32) rot[h][c] = cT.rotc[seat][c];
     }
-    int cnt = 0, src = 0;
+    int cnt = 0, src = 0, csrc = 0;   // csrc: the source's canonical compact index
     uint64_t m0 = 0, m1 = 0, m2 = 0;
     if (p < n) {
         const LegalRec &G = S.lg[env];
         src = G.src[p];
         m0 = G.mask[p][0]; m1 = G.mask[p][1]; m2 = G.mask[p][2];
         cnt = __popcll(m0) + __popcll(m1) + __popcll(m2);
+        if (mask_words) csrc = cT.canc[seat][src];
     }
     int incl = cnt;
     for (int o = 1; o < 32; o <<= 1) { const int v = __shfl_up(incl, o, 32); if (p >= o) incl += v; }
@@ -1344,7 +1345,7 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
         for (int step = 16; step >= 1; step >>= 1)
             if (j + step < n && start[h][j + step] <= i) j += step;
         const uint64_t w0 = __shfl(m0, j, 32), w1 = __shfl(m1, j, 32), w2 = __shfl(m2, j, 32);
-        const int s = __shfl(src, j, 32);
+        const int s = __shfl(src, j, 32), cs = __shfl(csrc, j, 32);
         if (i < total) {
             const int k = i - start[h][j];
             const int c0 = __popcll(w0), c1 = __popcll(w1);
@@ -1352,7 +1353,7 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
                                  : k < c0 + c1 ? 64 + select64(w1, k - c0) : 128 + select64(w2, k - c0 - c1);
             if ((int64_t)base + i < cap) values[base + i] = s * NC + c2f[c];
             if (mask_words) {   // canonical bit (rotated source) * 129 + (rotated destination)
-                const int bit = rot[h][flat_rank(cT.onm, s)] * NONB + rot[h][c];
+                const int bit = cs * NONB + rot[h][c];
                 atomicOr(&mbits[h][bit >> 5], 1u << (bit & 31));
             }
         }
@@ -1510,7 +1511,7 @@ __device__ __forceinline__ int32_t sample_logits_wave(int env, int l, int seat, 
     for (int j = l; j < c; j += 64) {
         const int32_t w = values[off + j];
         const int src = w / NC, dst = w - src * NC;
-        const int cc = (int)cT.rotc[seat][cT.f2c[src]] * NONB + (int)cT.rotc[seat][cT.f2c[dst]];
+        const int cc = (int)cT.canc[seat][src] * NONB + (int)cT.canc[seat][dst];
         const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), (uint32_t)(1 + cc),
                                          (uint32_t)seed, (uint32_t)(seed >> 32));
         const uint64_t key = ((uint64_t)u << 32) | (uint32_t)~(uint32_t)cc;   // > 0 for every real id

@@ -170,8 +170,10 @@ void build_tables(Tables &t)
             t.rot[s][f] = (int16_t)(cy * 17 + cx);
             t.unrot[s][cy * 17 + cx] = (int16_t)f;
         }
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < 4; ++s) {
         for (int i = 0; i < NONB; ++i) t.rotc[s][i] = (uint8_t)t.f2c[t.rot[s][t.c2f[i]]];
+        for (int f = 0; f < NC; ++f) t.canc[s][f] = t.f2c[f] >= 0 ? t.rotc[s][t.f2c[f]] : (uint8_t)0xFF;
+    }
     for (int p = 0; p < NP; ++p) {
         const int s = p / 30, i = p % 30;
         int x, y; seat_cell(s, i, x, y);

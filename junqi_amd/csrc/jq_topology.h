@@ -55,6 +55,7 @@ struct Tables {
     // 289-bit flat masks: a cell's compact index is the number of on-board
     // cells below it, its rail index the number of rail cells below it
     uint64_t onm[5], railm[5], shm[5];
+    uint8_t canc[4][NC];          // world flat -> canonical compact of observer s (0xFF off board)
 };
 
 void build_tables(Tables &t);

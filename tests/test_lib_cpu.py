@@ -62,7 +62,7 @@ _TABLES = _struct([
     ("localidx", "i1", (289,)),
     ("adjc", "u1", (129, 8), 8), ("raym", "<u8", (73, 4, 3)), ("crayc", "u1", (73, 2, 16), 16),
     ("railc", "u1", (73,)), ("railidxc", "i1", (129,)), ("campm", "<u8", (3,)), ("onm", "<u8", (5,)),
-    ("railm", "<u8", (5,)), ("shm", "<u8", (5,)),
+    ("railm", "<u8", (5,)), ("shm", "<u8", (5,)), ("canc", "u1", (4, 289)),
 ])
 
 
@@ -90,6 +90,10 @@ def test_board_tables_equal_oracle(jl):
     assert np.array_equal((fl & 32) > 0, o["arc"] > 0)
     assert np.array_equal(fl >> 8, o["curve"])
     assert np.array_equal(t["c2f"], o["compact_to_flat"])
+    # world flat -> canonical compact: the composition of f2c and rotc
+    on = t["f2c"] >= 0
+    for s in range(4):
+        assert np.array_equal(t["canc"][s][on], t["rotc"][s][t["f2c"][on]]) and (t["canc"][s][~on] == 255).all()
     # rail graph: the 73-bit neighbour masks against the oracle adjacency lists
     for i in range(73):
         f = int(t["railcell"][i])
