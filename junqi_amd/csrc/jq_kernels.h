@@ -172,62 +172,17 @@ __device__ __forceinline__ void env_boards(const int8_t *cell, int team, BB &occ
 }
 
 // Road steps and, for non-engineers on a rail, straight runs and curve runs of
-// the piece on compact cell sc (rail index r or -1); lane-local
-// (move_gen.py:1052-1199 parts a, b, c, e). land = empty or attackable.
-__device__ __forceinline__ BB piece_moves_bb(int sc, int r, bool engineer, const BB &occ, const BB &ea)
-{
-    const BB land = {~occ.w0 | ea.w0, ~occ.w1 | ea.w1, (~occ.w2 | ea.w2) & 1ull};
-    BB m = {0, 0, 0};
-    const uint64_t nb8 = *reinterpret_cast<const uint64_t *>(cT.adjc[sc]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int c = (int)((nb8 >> (8 * j)) & 0xFF);
-        if (c != 0xFF && bb_has(land, c)) setbit3(m.w0, m.w1, m.w2, c);
-    }
-    if (engineer || r < 0) return m;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const BB run = {cT.raym[r][k][0], cT.raym[r][k][1], cT.raym[r][k][2]};
-        const BB blk = bb_and(run, occ);
-        if (!bb_any(blk)) {
-            m = bb_or(m, run);
-        } else {   // cells before the first occupied one, plus that one if attackable
-            const int f = (k & 1) ? bb_highest(blk) : bb_lowest(blk);
-            m = bb_or(m, bb_and(run, (k & 1) ? bb_above(f) : bb_below(f)));
-            if (bb_has(ea, f)) setbit3(m.w0, m.w1, m.w2, f);
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < 2; ++d) {
-        const uint4 q = *reinterpret_cast<const uint4 *>(cT.crayc[r][d]);
-        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-        bool open = true;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) {
-            const int c = (int)((qw[i >> 2] >> (8 * (i & 3))) & 0xFF);
-            if (!open || c == 0xFF) { open = false; continue; }
-            if (!bb_has(occ, c)) { setbit3(m.w0, m.w1, m.w2, c); continue; }
-            if (bb_has(ea, c)) setbit3(m.w0, m.w1, m.w2, c);
-            open = false;
-        }
-    }
-    return m;
-}
-
-// Half h (0 or 1) of the lane-local moves of piece_moves_bb, so two lanes
-// share one piece: neighbours 4h .. 4h + 3 of adjc, the +x / -x (h = 0) or
-// +y / -y (h = 1) straight runs, and curve run h. The union of both halves is
-// piece_moves_bb.
+// the piece on compact cell sc (rail index r or -1), lane-local
+// (move_gen.py:1052-1199 parts a, b, c, e), split in two halves so two lanes
+// share one piece: half h takes road / camp neighbours 4h .. 4h + 3 of adjc,
+// the +x / -x (h = 0) or +y / -y (h = 1) straight runs, and curve run h. The
+// union of both halves is the piece's move set. land = empty or attackable.
 __device__ __forceinline__ BB piece_moves_half(int sc, int r, bool engineer, int h, const BB &occ, const BB &ea)
 {
     const BB land = {~occ.w0 | ea.w0, ~occ.w1 | ea.w1, (~occ.w2 | ea.w2) & 1ull};
-    BB m = {0, 0, 0};
-    const uint32_t nb4 = reinterpret_cast<const uint32_t *>(cT.adjc[sc])[h];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int c = (int)((nb4 >> (8 * j)) & 0xFF);
-        if (c != 0xFF && bb_has(land, c)) setbit3(m.w0, m.w1, m.w2, c);
-    }
+    // this half's road / camp neighbours that are empty or attackable
+    const uint64_t *am = cT.adjm[sc][h];
+    BB m = {am[0] & land.w0, am[1] & land.w1, am[2] & land.w2};
     if (engineer || r < 0) return m;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {   // k = 2h + j; j = 0 runs toward higher compact indices

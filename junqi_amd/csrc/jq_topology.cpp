@@ -199,6 +199,13 @@ void build_tables(Tables &t)
         for (int k = 0; k < 4; ++k) if (t.diag[f][k] >= 0) t.adjc[c][n++] = (uint8_t)t.f2c[t.diag[f][k]];
         if (flags(f) & CF_CAMP) t.campm[c >> 6] |= 1ull << (c & 63);
         t.railidxc[c] = t.railidx[f];
+        for (int h = 0; h < 2; ++h) {
+            for (int w = 0; w < 3; ++w) t.adjm[c][h][w] = 0;
+            for (int j = 4 * h; j < 4 * h + 4; ++j) {
+                const int d = t.adjc[c][j];
+                if (d != 0xFF) t.adjm[c][h][d >> 6] |= 1ull << (d & 63);
+            }
+        }
     }
     std::memset(t.onm, 0, sizeof t.onm);
     std::memset(t.railm, 0, sizeof t.railm);

@@ -47,6 +47,7 @@ struct Tables {
     // compact cell c; compact order is flat order, so a straight run's cells
     // rise (+x, +y) or fall (-x, -y) in compact index)
     alignas(8) uint8_t adjc[NONB][8];     // road neighbours then camp diagonals, compact (0xFF none)
+    uint64_t adjm[NONB][2][3];            // adjc[c][4h .. 4h + 3] as a 129-bit set, h = 0, 1
     uint64_t raym[NRAIL][4][3];           // straight runs (+x, -x, +y, -y) as compact masks
     alignas(16) uint8_t crayc[NRAIL][2][16];  // curve runs in walk order, compact (0xFF pad)
     uint8_t railc[NRAIL];                 // rail index -> compact

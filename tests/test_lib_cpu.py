@@ -60,7 +60,7 @@ _TABLES = _struct([
     ("rot", "<i2", (4, 289)), ("unrot", "<i2", (4, 289)), ("rotc", "u1", (4, 129)), ("home", "<i2", (120,)),
     ("slotch", "i1", (30,)), ("statics", "u1", (289,)), ("sh_other", "<i2", (289,)), ("owner", "i1", (289,)),
     ("localidx", "i1", (289,)),
-    ("adjc", "u1", (129, 8), 8), ("raym", "<u8", (73, 4, 3)), ("crayc", "u1", (73, 2, 16), 16),
+    ("adjc", "u1", (129, 8), 8), ("adjm", "<u8", (129, 2, 3)), ("raym", "<u8", (73, 4, 3)), ("crayc", "u1", (73, 2, 16), 16),
     ("railc", "u1", (73,)), ("railidxc", "i1", (129,)), ("campm", "<u8", (3,)), ("onm", "<u8", (5,)),
     ("railm", "<u8", (5,)), ("shm", "<u8", (5,)), ("canc", "u1", (4, 289)),
 ])
@@ -149,6 +149,9 @@ def test_compact_move_tables(jl):
         want = {int(f2c[v]) for v in t["adj"][f] if v >= 0} | {int(f2c[v]) for v in t["diag"][f] if v >= 0}
         got = [int(v) for v in t["adjc"][c] if v != 0xFF]
         assert len(got) == len(set(got)) and set(got) == want, c
+        for h in range(2):   # each half's neighbours as a bit set
+            half = {int(v) for v in t["adjc"][c][4 * h: 4 * h + 4] if v != 0xFF}
+            assert set(np.flatnonzero(_bits(t["adjm"][c][h], 129))) == half, (c, h)
     for i in range(73):
         src = int(f2c[t["railcell"][i]])
         for k in range(4):
