@@ -28,7 +28,22 @@ constexpr int LSCR_WORDS = 12;   // legal_body's per-wave LDS scratch (u64 words
 
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ uint16_t cflags(int f) { return cT.cflags[f]; }
+
+// Entry i of a byte or halfword table in cT, read through the aligned 32-bit
+// word that holds it. At a wave-uniform index this is a scalar load (there are
+// none for bytes or halfwords), which neither waits for nor is waited for by
+// the wave's vector stores; at a per-lane index it is an ordinary vector load.
+template <typename T>
+__device__ __forceinline__ T tab(const T *table, int i)
+{
+    static_assert(sizeof(T) <= 2, "byte and halfword tables only");
+    typedef const __attribute__((address_space(4))) uint32_t *const_word;   // constant memory
+    const uintptr_t a = reinterpret_cast<uintptr_t>(table + i);
+    const uint32_t w = *reinterpret_cast<const_word>(a & ~uintptr_t(3));
+    return (T)(w >> (8 * (a & 3)));
+}
+
+__device__ __forceinline__ uint16_t cflags(int f) { return tab(cT.cflags, f); }
 __device__ __forceinline__ bool is_on(int f) { return cflags(f) & CF_ON; }
 __device__ __forceinline__ bool is_rail(int f) { return cflags(f) & CF_RAIL; }
 __device__ __forceinline__ bool is_camp(int f) { return cflags(f) & CF_CAMP; }
@@ -296,16 +311,35 @@ __device__ void piece_mask_lane(const int8_t *cell, int src, int team, bool engi
 }
 
 // dst on a straight run (k < 4) or curve run of src with every earlier cell empty
-// (move_gen.py:127-171 and 384-423).
+// (move_gen.py:127-171 and 384-423). Wave-uniform: table reads are scalar loads.
+// A straight move stays on src's row or column, so only the run toward dst is
+// walked; its 12 entries come in with one batch of word loads.
 __device__ __forceinline__ bool run_clear(const int8_t *cell, int src, int dst, bool curve)
 {
-    const int r = cT.railidx[src];
+    typedef const __attribute__((address_space(4))) uint32_t *const_word;
+    const int r = tab(cT.railidx, src);
     if (r < 0) return false;
-    const int nruns = curve ? 2 : 4;
-    for (int k = 0; k < nruns; ++k) {
-        const int len = curve ? cT.craylen[r][k] : cT.raylen[r][k];
+    if (!curve) {
+        const int sx = src % 17, sy = src / 17, dx = dst % 17, dy = dst / 17;
+        const int k = sy == dy ? (dx > sx ? 0 : 1) : (dy > sy ? 2 : 3);   // +x, -x, +y, -y
+        const int len = tab(&cT.raylen[r][0], k);
+        const_word rw = reinterpret_cast<const_word>(reinterpret_cast<uintptr_t>(cT.rays[r][k]));
+        uint32_t w[6];
+#pragma unroll
+        for (int j = 0; j < 6; ++j) w[j] = rw[j];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            if (i >= len) break;
+            const int nb = (int16_t)(w[i >> 1] >> (16 * (i & 1)));
+            if (nb == dst) return true;
+            if (__builtin_amdgcn_readfirstlane(cell[nb]) >= 0) return false;
+        }
+        return false;
+    }
+    for (int k = 0; k < 2; ++k) {
+        const int len = tab(&cT.craylen[r][0], k);
         for (int i = 0; i < len; ++i) {
-            const int nb = curve ? cT.crays[r][k][i] : cT.rays[r][k][i];
+            const int nb = tab(&cT.crays[r][k][0], i);
             if (nb == dst) return true;
             if (__builtin_amdgcn_readfirstlane(cell[nb]) >= 0) break;
         }
@@ -317,9 +351,9 @@ __device__ __forceinline__ bool engineer_reaches(const int8_t *cell, int src, in
 {   // move_gen.py:186-224: dst is adjacent to the closure of src
     if (!is_rail(src) || !is_rail(dst) || src == dst) return false;
     uint64_t r0, r1;
-    const int dr = cT.railidx[dst];
+    const int dr = tab(cT.railidx, dst);
     const uint64_t t0 = cT.rnbr[dr][0], t1 = cT.rnbr[dr][1];
-    rail_closure(cell, cT.railidx[src], r0, r1, t0, t1);
+    rail_closure(cell, tab(cT.railidx, src), r0, r1, t0, t1);
     return ((t0 & r0) | (t1 & r1)) != 0;
 }
 
@@ -604,8 +638,8 @@ __device__ __forceinline__ void belief_update(const State &S, int env, const int
     }
     if (fcap) {
         trk &= (uint8_t)~(1u << ds);
-    } else if (ev == EV_EAT && dp >= 0 && is_sh(dst) && cT.owner[dst] == ds) {
-        const int other = cT.sh_other[dst];
+    } else if (ev == EV_EAT && dp >= 0 && is_sh(dst) && tab(cT.owner, dst) == ds) {
+        const int other = tab(cT.sh_other, dst);
         const int op = cell[other];
         if (op >= 0 && !code_onehot(bc[op])) bc[op] = (uint8_t)(1 + (T_JUNQI - 2));
     }
