@@ -694,7 +694,18 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     else step_load(S, env, l, ld);
     const int8_t *cv = ld.cv;
     const PieceRec &r0 = ld.r0, &r1 = ld.r1;
-    const EnvRec &E = S.env[env];   // uniform: scalar loads
+    // the env record, read once before any store of the ply (a later read
+    // would wait for the ply's stores) into scalar registers
+    EnvRec E;
+    {
+        const uint4 *er = reinterpret_cast<const uint4 *>(&S.env[env]);
+        const uint4 a0 = er[0], a1 = er[1];
+        const uint32_t w[8] = {(uint32_t)__builtin_amdgcn_readfirstlane(a0.x), (uint32_t)__builtin_amdgcn_readfirstlane(a0.y),
+                               (uint32_t)__builtin_amdgcn_readfirstlane(a0.z), (uint32_t)__builtin_amdgcn_readfirstlane(a0.w),
+                               (uint32_t)__builtin_amdgcn_readfirstlane(a1.x), (uint32_t)__builtin_amdgcn_readfirstlane(a1.y),
+                               (uint32_t)__builtin_amdgcn_readfirstlane(a1.z), (uint32_t)__builtin_amdgcn_readfirstlane(a1.w)};
+        __builtin_memcpy(&E, w, sizeof E);
+    }
 #pragma unroll
     for (int k = 0; k < 5; ++k)
         if (l + 64 * k < CELL_STRIDE) cell[l + 64 * k] = cv[k];
@@ -709,10 +720,10 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     a = __builtin_amdgcn_readfirstlane(a);   // wave-uniform: the ply's scalar work stays on the SALU
     int src = -1, dst = -1;
     if (act_fmt == 1) {
-        const int as = acting ? acting[env] : seat;
+        const int as = __builtin_amdgcn_readfirstlane(acting ? (int)acting[env] : seat);
         if (a >= 0 && a < NONB * NONB && as >= 0 && as < 4) {
-            src = cT.unrot[as][cT.c2f[a / NONB]];
-            dst = cT.unrot[as][cT.c2f[a % NONB]];
+            src = tab(cT.unrot[as], tab(cT.c2f, a / NONB));
+            dst = tab(cT.unrot[as], tab(cT.c2f, a % NONB));
         }
     } else if (a >= 0 && a < NC * NC) {
         src = a / NC; dst = a % NC;
