@@ -444,12 +444,18 @@ __device__ __forceinline__ int resolve_combat(int a, int d)
     return a < d ? EV_EAT : EV_KILLED;
 }
 
+// The Zobrist key table is written only by its upload, never by a kernel, so
+// kernels read it as constant memory: a wave-uniform key is then a scalar load,
+// which does not wait behind the wave's vector stores.
+typedef const __attribute__((address_space(4))) uint64_t *KeyTable;
+__device__ __forceinline__ KeyTable keys(const uint64_t *z) { return reinterpret_cast<KeyTable>(reinterpret_cast<uintptr_t>(z)); }
+
 __device__ __forceinline__ uint64_t zp(const uint64_t *z, int pid, int t, int f)
 {   // indexes come from state rows; out-of-range values read entry 0 instead of faulting
     pid = (unsigned)pid < 120u ? pid : 0;
     t = (unsigned)t < 14u ? t : 0;
     f = (unsigned)f < 289u ? f : 0;
-    return z[((size_t)pid * 14 + t) * 289 + f];
+    return keys(z)[((size_t)pid * 14 + t) * 289 + f];
 }
 
 __device__ __forceinline__ int tracked(int t) { return (t >= 2 && t <= 13) ? t - 2 : -1; }
@@ -738,7 +744,7 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
 
     const int mc0 = E.mc, mslc0 = E.mslc;
     uint64_t zob = E.zob;
-    const uint64_t *Z = S.ztab;
+    const KeyTable Z = keys(S.ztab);
     zob ^= Z[ZOFF_TURN + seat] ^ Z[ZOFF_MC + (mc0 & 0xFFF)] ^ Z[ZOFF_MSLC + (mslc0 & 0x1FF)];
     const int step = mc0 + 1;
     int died = 0;
@@ -962,7 +968,7 @@ __device__ void init_env(const State &S, int env, const int8_t *types, int8_t *l
         S.env[env].remtrk[l] = trk;
     }
     if (l == 0) {
-        const uint64_t *Z = S.ztab;
+        const KeyTable Z = keys(S.ztab);
         z ^= Z[ZOFF_TURN + 0] ^ Z[ZOFF_MC + 0] ^ Z[ZOFF_MSLC + 0] ^ Z[ZOFF_WIN + 0] ^ Z[ZOFF_SHOW + S.show_mode];
         EnvRec &W = S.env[env];
         W.zob = z; W.mc = 0; W.mslc = 0; W.hmeta = 0;
@@ -1036,7 +1042,7 @@ __global__ __launch_bounds__(64) void k_finalize(State S, int beliefs, const uin
         S.env[env].remtrk[l] = trk;
     }
     if (l == 0) {
-        const uint64_t *Z = S.ztab;
+        const KeyTable Z = keys(S.ztab);
         const EnvRec &E = S.env[env];
         const int w = E.winner;
         z ^= Z[ZOFF_TURN + (E.turn & 3)] ^ Z[ZOFF_MC + (E.mc & 0xFFF)] ^ Z[ZOFF_MSLC + (E.mslc & 0x1FF)];
