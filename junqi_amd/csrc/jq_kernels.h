@@ -44,6 +44,29 @@ __device__ __forceinline__ T tab(const T *table, int i)
 }
 
 __device__ __forceinline__ uint16_t cflags(int f) { return tab(cT.cflags, f); }
+
+// A 32-bit word of global memory at a wave-uniform address, read as a scalar
+// load. Only for a word no wave writes before this read in the same kernel
+// (an env's CSR count and offset are rewritten only by that env's own wave,
+// after it has read them): the scalar cache is not coherent with vector stores.
+__device__ __forceinline__ int32_t uniform_word(const int32_t *p)
+{
+    typedef const __attribute__((address_space(4))) int32_t *const_i32;
+    return *reinterpret_cast<const_i32>(reinterpret_cast<uintptr_t>(p));
+}
+
+// An env's 32-byte record as one scalar load: only the env's own wave writes it,
+// after reading it.
+__device__ __forceinline__ EnvRec env_record(const State &S, int env)
+{
+    const int32_t *w = reinterpret_cast<const int32_t *>(S.env + env);
+    int32_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = uniform_word(w + k);
+    EnvRec E;
+    __builtin_memcpy(&E, v, sizeof E);
+    return E;
+}
 __device__ __forceinline__ bool is_on(int f) { return cflags(f) & CF_ON; }
 __device__ __forceinline__ bool is_rail(int f) { return cflags(f) & CF_RAIL; }
 __device__ __forceinline__ bool is_camp(int f) { return cflags(f) & CF_CAMP; }
@@ -700,18 +723,9 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     else step_load(S, env, l, ld);
     const int8_t *cv = ld.cv;
     const PieceRec &r0 = ld.r0, &r1 = ld.r1;
-    // the env record, read once before any store of the ply (a later read
-    // would wait for the ply's stores) into scalar registers
-    EnvRec E;
-    {
-        const uint4 *er = reinterpret_cast<const uint4 *>(&S.env[env]);
-        const uint4 a0 = er[0], a1 = er[1];
-        const uint32_t w[8] = {(uint32_t)__builtin_amdgcn_readfirstlane(a0.x), (uint32_t)__builtin_amdgcn_readfirstlane(a0.y),
-                               (uint32_t)__builtin_amdgcn_readfirstlane(a0.z), (uint32_t)__builtin_amdgcn_readfirstlane(a0.w),
-                               (uint32_t)__builtin_amdgcn_readfirstlane(a1.x), (uint32_t)__builtin_amdgcn_readfirstlane(a1.y),
-                               (uint32_t)__builtin_amdgcn_readfirstlane(a1.z), (uint32_t)__builtin_amdgcn_readfirstlane(a1.w)};
-        __builtin_memcpy(&E, w, sizeof E);
-    }
+    // the env record, read once into scalar registers before any store of the
+    // ply (only this wave writes it, at the end)
+    const EnvRec E = env_record(S, env);
 #pragma unroll
     for (int k = 0; k < 5; ++k)
         if (l + 64 * k < CELL_STRIDE) cell[l + 64 * k] = cv[k];
@@ -1476,9 +1490,9 @@ __device__ __forceinline__ int32_t sample_pick(int env, const int32_t *__restric
                                                const int32_t *__restrict__ offsets, const int32_t *__restrict__ values,
                                                int64_t cap, uint64_t seed, uint64_t ply)
 {
-    const int c = counts[env];
+    const int c = uniform_word(counts + env);
     if (c <= 0) return -1;
-    const int64_t off = offsets[env];
+    const int64_t off = uniform_word(offsets + env);
     if (off < 0 || off + c > cap) return -1;
     const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
                                      (uint32_t)seed, (uint32_t)(seed >> 32));
@@ -1508,9 +1522,9 @@ __device__ __forceinline__ int32_t sample_logits_wave(int env, int l, int seat, 
                                                       uint64_t ply, int &canon)
 {
     canon = -1;
-    const int c = counts[env];
+    const int c = uniform_word(counts + env);
     if (c <= 0 || seat < 0 || seat > 3) return -1;
-    const int64_t off = offsets[env];
+    const int64_t off = uniform_word(offsets + env);
     if (off < 0 || off + c > cap) return -1;
     uint64_t best = 0;
     int32_t bw = -1;
@@ -1593,7 +1607,7 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
         a = A.actions[env];
     } else if (A.sampler == 1) {
         int cc;
-        a = sample_logits_wave(env, l, S.env[env].turn, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed,
+        a = sample_logits_wave(env, l, env_record(S, env).turn, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed,
                                A.ply, cc);
     } else {
         a = sample_pick(env, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed, A.ply);
