@@ -93,21 +93,16 @@ __device__ __forceinline__ void setbit3(uint64_t &m0, uint64_t &m1, uint64_t &m2
     m2 |= (w == 2) ? b : 0ull;
 }
 
-__device__ __forceinline__ uint64_t wave_or(uint64_t v)
-{
-    for (int o = 32; o > 0; o >>= 1) v |= (uint64_t)__shfl_xor((long long)v, o);
-    return v;
-}
-__device__ __forceinline__ uint64_t wave_xor(uint64_t v)
-{
-    for (int o = 32; o > 0; o >>= 1) v ^= (uint64_t)__shfl_xor((long long)v, o);
-    return v;
-}
-__device__ __forceinline__ int wave_sum(int v)
-{
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
+// Whole-wave reductions (every lane active), from the ROCm device library's
+// wavefront reductions (DPP / lane permutes instead of six LDS shuffles).
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_or_u64(unsigned long long);
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_xor_u64(unsigned long long);
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(unsigned long long);
+extern "C" __device__ __attribute__((const)) int __ockl_wfred_add_i32(int);
+__device__ __forceinline__ uint64_t wave_or(uint64_t v) { return __ockl_wfred_or_u64(v); }
+__device__ __forceinline__ uint64_t wave_xor(uint64_t v) { return __ockl_wfred_xor_u64(v); }
+__device__ __forceinline__ uint64_t wave_max(uint64_t v) { return __ockl_wfred_max_u64(v); }
+__device__ __forceinline__ int wave_sum(int v) { return __ockl_wfred_add_i32(v); }
 
 // Reachability closure of an engineer standing on rail index `src_r`: the source
 // plus every rail node joined to it through empty rail cells. Lane l evaluates
@@ -1537,11 +1532,7 @@ __device__ __forceinline__ int32_t sample_logits_wave(int env, int l, int seat, 
         const uint64_t key = ((uint64_t)u << 32) | (uint32_t)~(uint32_t)cc;   // > 0 for every real id
         if (key > best) { best = key; bw = w; }
     }
-    uint64_t m = best;
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint64_t v = __shfl_xor(m, o);
-        m = v > m ? v : m;
-    }
+    const uint64_t m = wave_max(best);
     const uint64_t who = __ballot(best == m && bw >= 0);
     const int src_lane = who ? __builtin_ctzll(who) : 0;
     canon = (int)~(uint32_t)(m & 0xFFFFFFFFu);
