@@ -445,7 +445,7 @@ __device__ __forceinline__ bool seat_has_move(const int8_t *cell, const int16_t 
     while (engs) {
         const int e = __builtin_ctzll(engs);
         engs &= engs - 1;
-        const int esrc = __shfl(src, e);
+        const int esrc = __builtin_amdgcn_readlane(src, e);   // e is wave-uniform
         uint64_t e0, e1, e2;
         engineer_mask(cell, esrc, team, e0, e1, e2);
         if (e0 | e1 | e2) return true;
@@ -1126,7 +1126,7 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
             lanes[j] = engs ? __builtin_ctzll(engs) : 64;
             ne += engs ? 1 : 0;
             engs &= engs - 1;
-            sr[j] = lanes[j] < 64 ? __shfl(ridx, lanes[j]) : -1;
+            sr[j] = lanes[j] < 64 ? __builtin_amdgcn_readlane(ridx, lanes[j]) : -1;   // uniform lane
         }
         if (l < 9) edst[l] = 0;
         engineers_bb(ne, sr, occ, ea, edst);
@@ -1263,7 +1263,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict
             int incl = s4;
             for (int o = 1; o < 64; o <<= 1) { const int u = __shfl_up(incl, o); if (lane >= o) incl += u; }
             excl[k] = segsum + incl - s4;
-            segsum += __shfl(incl, 63);
+            segsum += __builtin_amdgcn_readlane(incl, 63);
         }
         if (lane == 0) wsum[w] = segsum;
         __syncthreads();
@@ -1353,7 +1353,7 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
     const int base = live ? offsets[env] : 0;
     __syncthreads();
     // uniform trip count (the larger half's total): every lane takes the shuffles
-    const int trips = max(__shfl(total, 0), __shfl(total, 32));
+    const int trips = max(__builtin_amdgcn_readlane(total, 0), __builtin_amdgcn_readlane(total, 32));
     for (int b = 0; b < trips; b += 32) {
         const int i = b + p;
         int j = 0;   // piece of id i: the last piece whose start is <= i
@@ -1536,7 +1536,7 @@ __device__ __forceinline__ int32_t sample_logits_wave(int env, int l, int seat, 
     const uint64_t who = __ballot(best == m && bw >= 0);
     const int src_lane = who ? __builtin_ctzll(who) : 0;
     canon = (int)~(uint32_t)(m & 0xFFFFFFFFu);
-    return __shfl(bw, src_lane);
+    return __builtin_amdgcn_readlane(bw, src_lane);   // src_lane is wave-uniform
 }
 
 __global__ __launch_bounds__(64) void k_sample_logits(State S, const int8_t *__restrict__ acting,
