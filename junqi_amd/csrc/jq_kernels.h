@@ -29,6 +29,11 @@ constexpr int LSCR_WORDS = 12;   // legal_body's per-wave LDS scratch (u64 words
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+__device__ __forceinline__ uint32_t nib_to_bytes(uint32_t nib)
+{   // 4 bits -> 4 bytes of 0/1: the shifted copies land on disjoint bit positions
+    return __umul24(nib & 0xFu, 0x00204081u) & 0x01010101u;
+}
+
 // Entry i of a byte or halfword table in cT, read through the aligned 32-bit
 // word that holds it. At a wave-uniform index this is a scalar load (there are
 // none for bytes or halfwords), which neither waits for nor is waited for by
@@ -1187,17 +1192,10 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
         for (int i = l; i < head; i += 64) row[i] = (bits[i >> 5] >> (i & 31)) & 1;
         const int nchunks = (JQ_ACTION_DIM - head) / 16;
         for (int q = l; q < nchunks; q += 64) {
-            const int i0 = head + q * 16;
-            uint32_t v[4];
-            for (int k = 0; k < 4; ++k) {
-                uint32_t word = 0;
-                for (int b = 0; b < 4; ++b) {
-                    const int i = i0 + k * 4 + b;
-                    word |= ((bits[i >> 5] >> (i & 31)) & 1u) << (8 * b);
-                }
-                v[k] = word;
-            }
-            *reinterpret_cast<uint4 *>(row + i0) = make_uint4(v[0], v[1], v[2], v[3]);
+            const int i0 = head + q * 16;   // bits i0 .. i0 + 15 (word (i0 >> 5) + 1 <= 520)
+            const uint32_t v = __builtin_amdgcn_alignbit(bits[(i0 >> 5) + 1], bits[i0 >> 5], i0 & 31);
+            *reinterpret_cast<uint4 *>(row + i0) =
+                make_uint4(nib_to_bytes(v), nib_to_bytes(v >> 4), nib_to_bytes(v >> 8), nib_to_bytes(v >> 12));
         }
         for (int i = head + nchunks * 16 + l; i < JQ_ACTION_DIM; i += 64) row[i] = (bits[i >> 5] >> (i & 31)) & 1;
     }}

@@ -560,11 +560,6 @@ __device__ __forceinline__ uint32_t bit_window(const ObsLds &L, int e)
     return __builtin_amdgcn_alignbit(L.bits[(e >> 5) + 1], L.bits[e >> 5], e & 31);
 }
 
-__device__ __forceinline__ uint32_t nib_to_bytes(uint32_t nib)
-{   // 4 bits -> 4 bytes of 0/1: the shifted copies land on disjoint bit positions
-    return __umul24(nib & 0xFu, 0x00204081u) & 0x01010101u;
-}
-
 // One full 16-byte chunk whose first element is e0. `off` is the image offset
 // of e0 (IMG_ZERO when the chunk touches no image range).
 template <int FMT>
