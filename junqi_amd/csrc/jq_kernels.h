@@ -350,7 +350,6 @@ __device__ __forceinline__ bool run_clear(const int8_t *cell, int src, int dst, 
         uint32_t w[6];
 #pragma unroll
         for (int j = 0; j < 6; ++j) w[j] = rw[j];
-#pragma unroll
         for (int i = 0; i < 12; ++i) {
             if (i >= len) break;
             const int nb = (int16_t)(w[i >> 1] >> (16 * (i & 1)));
