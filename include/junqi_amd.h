@@ -154,11 +154,13 @@ int jq_step(jq_env *env, const int32_t *actions, const int8_t *acting, int32_t a
  * src*289+dst (move_gen.py:1199 order); mask_words: device int32 (N, 521) packed
  * canonical compact mask; mask_bool: device uint8 (N, 16641) (gpu_rollout.py:1220).
  * Any output may be NULL (offsets/values need counts). values_capacity >=
- * N*JQ_MAX_LEGAL can never overflow and the call stays asynchronous; a smaller
- * capacity makes the call read the total (offsets[N]) back, as the reference's
- * CSR call does (game_state.cu:1936-1948), and return JQ_E_CAPACITY without
- * writing values when the ids do not fit (counts and offsets are written). No
- * kernel writes past values_capacity. Replaces legal_action_ids_batch_csr
+ * N*JQ_MAX_LEGAL can never overflow, and for N <= 671,088 (where that bound fits
+ * the int32 offsets) the call stays asynchronous; otherwise the call reads the
+ * total (offsets[N]) back, as the reference's CSR call does
+ * (game_state.cu:1936-1948), and returns JQ_E_CAPACITY without writing values
+ * when the ids do not fit the buffer or their total exceeds INT32_MAX (offsets
+ * and counts are written; offsets[N] is then -1). No kernel writes outside
+ * values[0 .. values_capacity). Replaces legal_action_ids_batch_csr
  * (game_state.cu:1892-1962) and legal_mask_canonical_batch (game_state.cu:2291-2508). */
 int jq_legal(jq_env *env, const int8_t *acting, int32_t *counts, int32_t *offsets, int32_t *values,
              int64_t values_capacity, int32_t *mask_words, uint8_t *mask_bool, void *stream);
@@ -246,7 +248,7 @@ int jq_sample_logits(jq_env *env, const int8_t *acting, const int32_t *counts, c
  * observation). hash: device uint64 (N), each env's Zobrist hash after its ply
  * and before any restart; terminated / reward as jq_step's; actions_out the
  * action taken (world id, -1 none).
- * With a u8 observation and values_capacity >= N * JQ_MAX_LEGAL the CSR pass,
+ * With a u8 observation, values_capacity >= N * JQ_MAX_LEGAL and N <= 671,088 the CSR pass,
  * which then also writes the canonical mask words, runs on a library-owned
  * side stream beside the observation (they share no data); `stream` waits for
  * it before the call's work counts as done, so the call stays ordered on

@@ -54,14 +54,22 @@ __device__ __forceinline__ uint16_t cflags(int f) { return tab(cT.cflags, f); }
 // load. Only for a word no wave writes before this read in the same kernel
 // (an env's CSR count and offset are rewritten only by that env's own wave,
 // after it has read them): the scalar cache is not coherent with vector stores.
+// Loads through the constant address space count as invariant to the compiler,
+// which may then re-issue one at a later use instead of keeping its register;
+// after the wave's own store to the word that would read the new value. The
+// empty asm takes the loaded word as its output, which the compiler can only
+// keep (or spill), never recompute: every later use sees the value read here.
 __device__ __forceinline__ int32_t uniform_word(const int32_t *p)
 {
     typedef const __attribute__((address_space(4))) int32_t *const_i32;
-    return *reinterpret_cast<const_i32>(reinterpret_cast<uintptr_t>(p));
+    int32_t v = *reinterpret_cast<const_i32>(reinterpret_cast<uintptr_t>(p));
+    asm volatile("" : "+s"(v));
+    return v;
 }
 
 // An env's 32-byte record as one scalar load: only the env's own wave writes it,
-// after reading it.
+// after reading it (at the end of its ply or restart); every field keeps the
+// value read here (uniform_word).
 __device__ __forceinline__ EnvRec env_record(const State &S, int env)
 {
     const int32_t *w = reinterpret_cast<const int32_t *>(S.env + env);
@@ -1227,7 +1235,9 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
 // tile's 2048 counts from 2048 w on: lane l holds the four counts at 4 (64 k + l)
 // for k < 8, so every 16-byte load and store of the wave covers one contiguous
 // 1 KB; eight wave scans give the running sums, the 16 wave totals are scanned
-// through LDS, and a carry runs between tiles.
+// through LDS, and a carry runs between tiles. The carry is 64-bit: a total
+// beyond INT32_MAX (offsets are int32, as the reference's) writes offsets[n] =
+// -1, which the host reads as "does not fit" before any id is emitted.
 constexpr int SCAN_THREADS = 1024, SCAN_CHUNKS = 8, SCAN_TILE = SCAN_THREADS * 4 * SCAN_CHUNKS;
 __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                       int n)
@@ -1236,7 +1246,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict
     __shared__ int32_t tile_total;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const bool vec = ((reinterpret_cast<uintptr_t>(counts) | reinterpret_cast<uintptr_t>(offsets)) & 15) == 0;
-    int carry = 0;
+    int64_t carry = 0;
     for (int base = 0; base < n; base += SCAN_TILE) {
         const int seg = base + w * 64 * 4 * SCAN_CHUNKS;
         int4 v[SCAN_CHUNKS];
@@ -1272,12 +1282,12 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict
             if (lane == SCAN_THREADS / 64 - 1) tile_total = y;
         }
         __syncthreads();
-        const int wbase = carry + wsum[w];
+        const int64_t wbase = carry + wsum[w];   // a tile's sums fit int: 32,768 x JQ_MAX_LEGAL < 2^31
 #pragma unroll
         for (int k = 0; k < SCAN_CHUNKS; ++k) {
             const int i = seg + 4 * (64 * k + lane);
             int4 o;
-            o.x = wbase + excl[k];
+            o.x = (int)(wbase + excl[k]);
             o.y = o.x + v[k].x;
             o.z = o.y + v[k].y;
             o.w = o.z + v[k].z;
@@ -1293,7 +1303,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_scan(const int32_t *__restrict
         carry += tile_total;
         __syncthreads();
     }
-    if (t == 0) offsets[n] = carry;
+    if (t == 0) offsets[n] = carry > (int64_t)INT32_MAX ? -1 : (int)carry;
 }
 
 // Position of the k-th set bit (k < popcount) of a 64-bit word.
@@ -1363,7 +1373,7 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
             const int c0 = __popcll(w0), c1 = __popcll(w1);
             const int c = k < c0 ? select64(w0, k)
                                  : k < c0 + c1 ? 64 + select64(w1, k - c0) : 128 + select64(w2, k - c0 - c1);
-            if ((int64_t)base + i < cap) values[base + i] = s * NC + c2f[c];
+            if (base >= 0 && (int64_t)base + i < cap) values[base + i] = s * NC + c2f[c];
             if (mask_words) {   // canonical bit (rotated source) * 129 + (rotated destination)
                 const int bit = cs * NONB + rot[h][c];
                 atomicOr(&mbits[h][bit >> 5], 1u << (bit & 31));
@@ -1478,13 +1488,16 @@ __device__ __forceinline__ uint32_t philox4x32_10(uint32_t c0, uint32_t c1, uint
 // Uniform pick from env's CSR row: Philox4x32-10 word 0 of counter
 // (env, ply lo, ply hi, 0) under key (seed lo, seed hi), scaled to the count;
 // -1 for an empty row or one that does not lie inside the values buffer.
+// Uniform: env is the same on every lane of the wave (one env per wave), so the
+// count and offset are scalar loads; else one env per lane.
+template <bool Uniform>
 __device__ __forceinline__ int32_t sample_pick(int env, const int32_t *__restrict__ counts,
                                                const int32_t *__restrict__ offsets, const int32_t *__restrict__ values,
                                                int64_t cap, uint64_t seed, uint64_t ply)
 {
-    const int c = uniform_word(counts + env);
+    const int c = Uniform ? uniform_word(counts + env) : counts[env];
     if (c <= 0) return -1;
-    const int64_t off = uniform_word(offsets + env);
+    const int64_t off = Uniform ? uniform_word(offsets + env) : offsets[env];
     if (off < 0 || off + c > cap) return -1;
     const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
                                      (uint32_t)seed, (uint32_t)(seed >> 32));
@@ -1498,7 +1511,7 @@ __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_
 {
     const int env = blockIdx.x * blockDim.x + threadIdx.x;
     if (env >= n) return;
-    out[env] = sample_pick(env, counts, offsets, values, cap, seed, ply);
+    out[env] = sample_pick<false>(env, counts, offsets, values, cap, seed, ply);
 }
 
 // Masked-logit pick by env's wave (lane l): the legal ids of the CSR row, lane
@@ -1598,7 +1611,7 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
         a = sample_logits_wave(env, l, env_record(S, env).turn, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed,
                                A.ply, cc);
     } else {
-        a = sample_pick(env, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed, A.ply);
+        a = sample_pick<true>(env, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed, A.ply);
     }
     if (A.actions_out && l == 0) A.actions_out[env] = a;
     TurnAfter nx;

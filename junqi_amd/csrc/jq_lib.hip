@@ -221,12 +221,21 @@ int check_setups(const int8_t *host, size_t count, const char *what)
     return JQ_OK;
 }
 
-// CSR capacity check of jq_legal / jq_env_step: with a values buffer smaller
-// than N * JQ_MAX_LEGAL the total (offsets[n], just scanned on `s`) is read back
-// and must fit.
+// A values buffer of N * JQ_MAX_LEGAL ids always holds the CSR, and the int32
+// offsets cannot overflow while that bound is at most INT32_MAX (N <= 671,088):
+// then no read-back is needed.
+bool csr_always_fits(const jq_env *e, int64_t cap)
+{
+    const int64_t bound = (int64_t)e->S.n * JQ_MAX_LEGAL;
+    return bound <= (int64_t)INT32_MAX && cap >= bound;
+}
+
+// CSR capacity check of jq_legal / jq_env_step: unless csr_always_fits, the
+// total (offsets[n], just scanned on `s`; -1 when it exceeds the int32 offsets)
+// is read back and must fit.
 int csr_fits(jq_env *e, const int32_t *offsets, int64_t cap, hipStream_t s)
 {
-    if (cap >= (int64_t)e->S.n * JQ_MAX_LEGAL) return JQ_OK;
+    if (csr_always_fits(e, cap)) return JQ_OK;
     if (!e->total_host) {
         void *q = nullptr;
         if (hipHostMalloc(&q, sizeof(int32_t)) != hipSuccess) return fail(JQ_E_OOM, "pinned host word");
@@ -234,6 +243,8 @@ int csr_fits(jq_env *e, const int32_t *offsets, int64_t cap, hipStream_t s)
     }
     HIP_TRY(hipMemcpyAsync(e->total_host, offsets + e->S.n, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
+    if (*e->total_host < 0)
+        return fail(JQ_E_CAPACITY, "legal ids exceed the int32 offsets (more than %d in the batch)", INT32_MAX);
     if ((int64_t)*e->total_host > cap)
         return fail(JQ_E_CAPACITY, "legal ids need %d values, the buffer holds %lld", *e->total_host, (long long)cap);
     return JQ_OK;
@@ -685,7 +696,7 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
     A.do_reset = e->S.pool ? 1 : 0; A.reset_seed = reset_seed; A.counts = counts;
     // The overlapped form moves the CSR pass, and the canonical mask with it,
     // beside the observation (below); the step kernel then skips the mask.
-    const bool overlap = spatial && obs_fmt == JQ_OBS_U8 && values_capacity >= (int64_t)e->S.n * JQ_MAX_LEGAL;
+    const bool overlap = spatial && obs_fmt == JQ_OBS_U8 && csr_always_fits(e, values_capacity);
     A.mask_words = overlap ? nullptr : mask_words;
     // sample (unless actions are given), ply, restart from the pool and the
     // next seat's legal sets in one kernel
@@ -706,6 +717,19 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
         // a timing event goes before the release of the side stream, so the
         // observation's dispatch still follows the step directly
         if ((rc = obs_timing_begin(e, stream, &e->obs_t_end)) != 0) return rc;
+        // Whatever path leaves this block, an end event whose begin was recorded
+        // above and that the observation did not take is recorded here, so no
+        // later launch pairs with it.
+        struct CloseTiming {
+            jq_env *e; void *stream;
+            ~CloseTiming()
+            {
+                if (e->obs_t_end) {
+                    (void)hipEventRecord(e->obs_t_end, strm(stream));
+                    e->obs_t_end = nullptr;
+                }
+            }
+        } close_timing{e, stream};
         HIP_TRY(hipEventRecord(e->ev_step, strm(stream)));
         HIP_TRY(hipStreamWaitEvent(e->side, e->ev_step, 0));
         hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, e->side, counts, offsets, e->S.n);
@@ -715,10 +739,6 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
         if ((rc = launch_check("k_emit")) != 0) return rc;
         HIP_TRY(hipEventRecord(e->ev_csr, e->side));
         rc = jq_observe(e, nullptr, obs_fmt, 0, spatial, aux, global, stream);
-        if (e->obs_t_end) {   // the observation failed before its launch: close the timing pair
-            (void)hipEventRecord(e->obs_t_end, strm(stream));
-            e->obs_t_end = nullptr;
-        }
         HIP_TRY(hipStreamWaitEvent(strm(stream), e->ev_csr, 0));   // joined even if the observation failed
         return rc;
     }

@@ -16,7 +16,10 @@ It records what no reference golden file, known-answer test or invariant pins
   BRIGHT, DARK and HALF_DARK, including DARK teammate beliefs after the
   opening (info_model.py:218-561);
 * bit-exact digests of all four observers' observations
-  (observation.py:621-857) at those plies.
+  (observation.py:621-857) at those plies;
+* before every ply and at the end, the acting seat's legal set
+  (GameState.legal_actions, state.py:1200-1213) as its size and a digest of
+  its sorted world ids src_flat*289 + dst_flat (legal_digest below).
 
 Games: setups from generate_random_setup(random.Random(seed)), actions by
 random.Random(seed + 1000).choice over GameState.legal_actions(), all four
@@ -48,6 +51,15 @@ def sha(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
 
+def legal_digest(ids) -> str:
+    """First 16 hex digits of the SHA-256 of the sorted ids as little-endian int32."""
+    return sha(np.sort(np.asarray(ids, dtype="<i4")))[:16]
+
+
+def world_ids(actions) -> list[int]:
+    return [(a.src[1] * 17 + a.src[0]) * 289 + a.dst[1] * 17 + a.dst[0] for a in actions]
+
+
 def main(ref_root: str) -> None:
     sys.path.insert(0, ref_root)
     from junqi_core.info_model import BeliefTensor
@@ -66,7 +78,7 @@ def main(ref_root: str) -> None:
             rng = random.Random(seed + 1000)
             rec = {"seed": seed, "show_mode": mode_name,
                    "setup": [int(p) for lu in setup for p in lu],
-                   "actions": [], "zobrist": [], "checkpoints": []}
+                   "actions": [], "zobrist": [], "legal_count": [], "legal_digest": [], "checkpoints": []}
 
             def checkpoint(ply: int) -> None:
                 cm = state.combat_memory
@@ -85,11 +97,17 @@ def main(ref_root: str) -> None:
                     cp["glob_f32"].append(sha(np.asarray(obs.global_, np.float32)))
                 rec["checkpoints"].append(cp)
 
+            def record_legal(legal) -> None:
+                ids = world_ids(legal)
+                rec["legal_count"].append(len(ids))
+                rec["legal_digest"].append(legal_digest(ids))
+
             checkpoint(0)
             for ply in range(1, MAX_PLIES + 1):
                 if state.terminated:
                     break
                 legal = state.legal_actions()
+                record_legal(legal)
                 if not legal:
                     break
                 a = rng.choice(legal)
@@ -101,6 +119,8 @@ def main(ref_root: str) -> None:
                 rec["zobrist"].append(format(int(state.zobrist) & (2**64 - 1), "016x"))
                 if ply in CHECKPOINTS:
                     checkpoint(ply)
+            if len(rec["legal_count"]) == len(rec["actions"]):   # the end position's set (empty once terminated)
+                record_legal(state.legal_actions())
             if rec["checkpoints"][-1]["ply"] != len(rec["actions"]):
                 checkpoint(len(rec["actions"]))
             rec["terminated"] = bool(state.terminated)

@@ -393,8 +393,10 @@ def _sha(a: np.ndarray) -> str:
 @pytest.mark.parametrize("mode", ["BRIGHT", "DARK", "HALF_DARK"])
 def test_reference_games_on_device(jq, mode):
     """The 12 complete games junqi_core played (tests/golden/reference_vectors.json):
-    the device's Zobrist hash after every ply and all four observers' float32
-    observations and globals at the recorded plies, bit for bit."""
+    the device's Zobrist hash after every ply, the acting seat's CSR legal row
+    before every ply and at the end (size and digest of the reference's
+    GameState.legal_actions), and all four observers' float32 observations and
+    globals at the recorded plies, bit for bit."""
     print(f"[boundary] reference games {mode}", flush=True)
     doc = json.loads((H.GOLDEN / "reference_vectors.json").read_text())
     recs = [r for r in doc["games"] if r["show_mode"] == mode]
@@ -416,8 +418,19 @@ def test_reference_games_on_device(jq, mode):
                 assert _sha(sp[i, s]) == cps[i][ply]["obs_f32"][s], f"game {i} ply {ply} observer {s}"
                 assert _sha(gl[i, s]) == cps[i][ply]["glob_f32"][s], f"game {i} ply {ply} globals {s}"
 
+    def check_legal(ply):   # the sets before ply + 1
+        b.legal()
+        offs = b.offsets.cpu().numpy()
+        vals = b.values[: int(offs[-1])].cpu().numpy()
+        for i, r in enumerate(recs):
+            if ply < len(r["legal_count"]):
+                row = vals[offs[i]:offs[i + 1]].astype("<i4")
+                assert len(row) == r["legal_count"][ply], f"game {i} before ply {ply + 1}: legal count"
+                assert _sha(row)[:16] == r["legal_digest"][ply], f"game {i} before ply {ply + 1}: legal set"
+
     check(0)
     for ply in range(1, plies + 1):
+        check_legal(ply - 1)
         acts = np.array([r["actions"][ply - 1][0] * 289 + r["actions"][ply - 1][1] if ply <= len(r["actions"])
                          else -1 for r in recs], np.int32)
         out = b.step(torch.from_numpy(acts).to(b.device))
@@ -428,5 +441,6 @@ def test_reference_games_on_device(jq, mode):
                 assert valid[i], f"game {i} ply {ply}: reference action rejected"
                 assert format(int(z[i]), "016x") == r["zobrist"][ply - 1], f"game {i} ply {ply}: Zobrist"
         check(ply)
+    check_legal(plies)
     assert [bool(t) for t in b.termination()["terminated"]] == [r["terminated"] for r in recs]
     b.close()

@@ -723,3 +723,142 @@ def test_vectorised_philox_helper_equals_oracle():
         got = G.philox_first_word_np(c0, c1, c2, c3, k0, k1)
         want = [O.philox4x32_10((int(a), c1, c2, c3), (k0, k1))[0] for a in c0]
         assert got.tolist() == want
+
+
+# ================================================================ termination
+# Q10 draw thresholds (tests/test_state_transitions.py:452-520; rules.py:444-445
+# MAX_NUM_MOVES = 4000, MAX_NUM_MOVES_BETWEEN_ATTACKS = 200, applied with >= in
+# _check_victory, state.py:1721-1724, before the turn advance, which is skipped
+# on termination, state.py:914-941) and the env's move cap
+# (tests/test_gpu_rollout.py:211-245; junqi_rl/env.py:295-305, applied after the
+# turn advance as game_state.cu:1651-1656 does).
+
+NO_CAP = 2**30   # GameState itself has no env cap
+_Q10 = [(SOUTH, "PAIZH", 8, 11), (WEST, "PAIZH", 5, 8), (NORTH, "PAIZH", 8, 0), (EAST, "PAIZH", 11, 8)]
+
+
+def _q10(mc, mslc, max_num_moves=NO_CAP, spec=_Q10):
+    return O.Game.from_pieces(_pieces(spec), turn=SOUTH, move_counter=mc, mslc=mslc,
+                              max_num_moves=max_num_moves)
+
+
+def _assert_draw(g, r, turn):
+    assert r["terminated"] == 1 and r["draw"] == 1 and r["winner"] == -1
+    assert g.terminated == 1 and g.draw == 1 and g.winner == -1
+    assert int(g.turn) == turn
+    assert int(g.zobrist) == g.recompute_zobrist()
+
+
+def _assert_live(g, r, turn):
+    assert r["terminated"] == 0 and r["draw"] == 0 and r["winner"] == -1
+    assert g.terminated == 0 and g.draw == 0
+    assert int(g.turn) == turn
+    assert int(g.zobrist) == g.recompute_zobrist()
+
+
+def test_q10_draw_by_move_counter():
+    """move_counter 3999 -> one move -> draw, no winner, rewards 0; the turn stays
+    with the mover (no advance on termination)."""
+    for cap in (NO_CAP, 4000):
+        g = _q10(3999, 0, cap)
+        r = _move(g, (8, 11), (8, 12))
+        assert r["event"] == 1
+        _assert_draw(g, r, SOUTH)
+        assert g.move_counter == 4000 and g.mslc == 1
+
+
+def test_q10_move_counter_below_threshold():
+    """A ply ending at move_counter 3999 does not draw; the turn advances."""
+    g = _q10(3998, 0)
+    r = _move(g, (8, 11), (8, 12))
+    _assert_live(g, r, WEST)
+    assert g.move_counter == 3999
+    rc, r = g.step_id(int(g.legal_ids()[0]))
+    assert rc == 0
+    _assert_draw(g, r, WEST)
+
+
+def test_q10_draw_by_no_combat_counter():
+    g = _q10(500, 199)
+    r = _move(g, (8, 11), (8, 12))
+    _assert_draw(g, r, SOUTH)
+    assert g.mslc == 200 and g.move_counter == 501
+
+
+def test_q10_no_combat_counter_below_threshold():
+    g = _q10(500, 198)
+    r = _move(g, (8, 11), (8, 12))
+    _assert_live(g, r, WEST)
+    assert g.mslc == 199
+
+
+def test_q10_draw_not_triggered_by_combat():
+    """Combat at moves_since_last_combat 199 resets the counter: no draw."""
+    spec = [(SOUTH, "SILING", 6, 11), (WEST, "PAIZH", 6, 10), (NORTH, "PAIZH", 8, 0), (EAST, "PAIZH", 11, 8)]
+    g = _q10(500, 199, spec=spec)
+    r = _move(g, (6, 11), (6, 10))
+    assert r["event"] == 2
+    assert g.mslc == 0 and g.move_counter == 501
+    # WEST lost its only piece, so it is dead and NORTH moves next
+    assert r["seats_died_mask"] == 1 << WEST
+    _assert_live(g, r, NORTH)
+
+
+def test_env_cap_one_and_three_moves():
+    """max_num_moves = 1 draws after one step; = 3 is live after one and two
+    steps and draws after three (tests/test_gpu_rollout.py:211-245). The cap
+    fires after the turn advance, so the turn has moved on."""
+    short = _q10(0, 0, 1)
+    r = _move(short, (8, 11), (8, 12))
+    _assert_draw(short, r, WEST)
+    longer = _q10(0, 0, 3)
+    for k in range(3):
+        seat = int(longer.turn)
+        ids = longer.legal_ids()
+        rc, r = longer.step_id(int(ids[0]))
+        assert rc == 0
+        nxt = (seat + 1) & 3
+        if k < 2:
+            _assert_live(longer, r, nxt)
+        else:
+            _assert_draw(longer, r, nxt)
+
+
+@pytest.mark.parametrize("cap", [1, 3, 600])
+def test_env_cap_below_and_at_limit(cap):
+    """A ply ending at cap - 1 is live; the ply ending at cap draws."""
+    g = _q10(cap - 2, 0, cap) if cap >= 2 else None
+    if g is not None:
+        r = _move(g, (8, 11), (8, 12))
+        _assert_live(g, r, WEST)
+        assert g.move_counter == cap - 1
+    g = _q10(cap - 1, 0, cap)
+    r = _move(g, (8, 11), (8, 12))
+    _assert_draw(g, r, WEST)
+
+
+def test_env_cap_survives_new_games():
+    """The limit is a property of the game's settings: a fresh game with the same
+    cap draws at the same ply again (reset_terminated_device keeps it)."""
+    setup = O.random_setup(100)
+    for cap, plies in ((1, 1), (3, 3)):
+        for _ in range(2):
+            g = O.Game(setup, max_num_moves=cap)
+            for k in range(plies):
+                assert not g.terminated
+                rc, r = g.step_id(int(g.legal_ids()[0]))
+                assert rc == 0
+            assert g.terminated and g.draw and g.winner == -1
+
+
+def test_rules_draw_and_cap_order():
+    """Rules draw (before the advance, turn frozen) vs env cap (after the
+    advance): the same ply from move_counter 3999 freezes the turn whatever the
+    cap, while a cap reached below 4000 moves the turn on."""
+    a = _q10(3999, 5, 4000)
+    b = _q10(3999, 5, NO_CAP)
+    c = _q10(2999, 5, 3000)
+    for g in (a, b, c):
+        _move(g, (8, 11), (8, 12))
+    assert int(a.turn) == SOUTH and int(b.turn) == SOUTH and int(c.turn) == WEST
+    assert int(a.zobrist) == int(b.zobrist)

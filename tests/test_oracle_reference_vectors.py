@@ -3,6 +3,8 @@
 tests/golden/reference_vectors.json holds 12 complete random games (seeds
 0-3 x BRIGHT / DARK / HALF_DARK, 613-803 plies each, every one played to a
 natural end) with, after every ply, the reference GameState's Zobrist hash
+the acting seat's legal set before every ply and at the end (its size and a
+digest of its sorted world ids, GameState.legal_actions, state.py:1200-1213),
 and, at plies 0, 60, 150, 250, 400, 600 and the last, digests of all sixteen
 combat-memory fields, every observer's BeliefTensor rows and remaining counts,
 and every observer's float32 observation and globals. The file is written by
@@ -41,6 +43,11 @@ def sha(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
 
+def legal_digest(ids: np.ndarray) -> str:
+    """The generator's digest: SHA-256 of the sorted ids as little-endian int32, 16 hex digits."""
+    return sha(np.sort(np.asarray(ids, dtype="<i4")))[:16]
+
+
 def check_point(g: O.Game, cp: dict, ctx: str) -> None:
     for ref_name, (name, dt) in CM_MAP.items():
         assert sha(np.asarray(g.buf[0][name]).astype(dt)) == cp["cm"][ref_name], f"{ctx}: combat memory {ref_name}"
@@ -65,10 +72,16 @@ def test_reference_game(rec):
     cps = {cp["ply"]: cp for cp in rec["checkpoints"]}
     check_point(g, cps[0], "ply 0")
     for ply, ((src, dst), z) in enumerate(zip(rec["actions"], rec["zobrist"]), start=1):
+        ids = g.legal_ids()
+        assert len(ids) == rec["legal_count"][ply - 1], f"before ply {ply}: legal count"
+        assert legal_digest(ids) == rec["legal_digest"][ply - 1], f"before ply {ply}: legal set"
         rc, _ = g.step(src, dst)
         assert rc == 0, f"ply {ply}: reference action rejected"
         assert format(int(g.zobrist), "016x") == z, f"ply {ply}: Zobrist hash"
         if ply in cps:
             check_point(g, cps[ply], f"ply {ply}")
     assert bool(g.terminated) == rec["terminated"]
+    ids = g.legal_ids()
+    assert len(rec["legal_count"]) == len(rec["actions"]) + 1
+    assert len(ids) == rec["legal_count"][-1] and legal_digest(ids) == rec["legal_digest"][-1], "end position"
     assert len(cps) >= 6

@@ -1,8 +1,8 @@
 """jq_history_reconstruct_noalloc through the C ABI on an MI355X: the same rows
 as jq_history_reconstruct (observations in f32 and u8 + aux, globals, packed
 and bool canonical masks), bit for bit, on two calls in a row, the second with
-a smaller batch; device memory does not move across the calls; a batch above
-the maximum is refused."""
+a smaller batch; device memory does not move across any of the calls, the
+first included; a batch above the maximum is refused."""
 
 from __future__ import annotations
 
@@ -74,8 +74,9 @@ def test_noalloc_reconstruct_equals_reconstruct(jq):
         for k in got:
             if got[k] is not None:
                 assert torch.equal(got[k], want[k]), f"batch {batch} {fmt}: {k} differs"
-        if batch != 900:   # the first call on the device may load the library's code object
-            assert free0 == free1, f"device memory moved by {free0 - free1} bytes in the no-allocation call"
+        # every call, the first included: the library's code object is resident
+        # (the rollout above launched its kernels), so any change is the call's own
+        assert free0 == free1, f"batch {batch} {fmt}: device memory moved by {free0 - free1} bytes in the no-allocation call"
     big = torch.zeros(L.NOALLOC_MAX_ROWS + 1, dtype=torch.int64, device=dev)
     bobs = torch.zeros(L.NOALLOC_MAX_ROWS + 1, dtype=torch.int8, device=dev)
     out = _outputs(dev, 1, "f32")
