@@ -59,11 +59,16 @@ __device__ __forceinline__ uint16_t cflags(int f) { return tab(cT.cflags, f); }
 // after the wave's own store to the word that would read the new value. The
 // empty asm takes the loaded word as its output, which the compiler can only
 // keep (or spill), never recompute: every later use sees the value read here.
-__device__ __forceinline__ int32_t uniform_word(const int32_t *p)
+__device__ __forceinline__ int32_t uniform_word_raw(const int32_t *p)
 {
     typedef const __attribute__((address_space(4))) int32_t *const_i32;
-    int32_t v = *reinterpret_cast<const_i32>(reinterpret_cast<uintptr_t>(p));
-    asm volatile("" : "+s"(v));
+    return *reinterpret_cast<const_i32>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ void pin_word(int32_t &v) { asm volatile("" : "+s"(v)); }
+__device__ __forceinline__ int32_t uniform_word(const int32_t *p)
+{
+    int32_t v = uniform_word_raw(p);
+    pin_word(v);
     return v;
 }
 
@@ -75,7 +80,9 @@ __device__ __forceinline__ EnvRec env_record(const State &S, int env)
     const int32_t *w = reinterpret_cast<const int32_t *>(S.env + env);
     int32_t v[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = uniform_word(w + k);
+    for (int k = 0; k < 8; ++k) v[k] = uniform_word_raw(w + k);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pin_word(v[k]);
     EnvRec E;
     __builtin_memcpy(&E, v, sizeof E);
     return E;
@@ -718,7 +725,7 @@ __device__ __forceinline__ void step_load(const State &S, int env, int l, StepLo
 
 __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t *__restrict__ acting, int act_fmt,
                          StepRes &res, int8_t *cell, int16_t *pos, int8_t *ptype, TurnAfter &nx,
-                         const StepLoad *pre = nullptr)
+                         const StepLoad *pre = nullptr, const EnvRec *pre_rec = nullptr)
 {
 
     // the board, the piece records, the env record and the action are all
@@ -731,8 +738,8 @@ __device__ void step_env(const State &S, int env, int l, int32_t a, const int8_t
     const int8_t *cv = ld.cv;
     const PieceRec &r0 = ld.r0, &r1 = ld.r1;
     // the env record, read once into scalar registers before any store of the
-    // ply (only this wave writes it, at the end)
-    const EnvRec E = env_record(S, env);
+    // ply (only this wave writes it, at the end), or handed in by the caller
+    const EnvRec E = pre_rec ? *pre_rec : env_record(S, env);
 #pragma unroll
     for (int k = 0; k < 5; ++k)
         if (l + 64 * k < CELL_STRIDE) cell[l + 64 * k] = cv[k];
@@ -1495,9 +1502,18 @@ __device__ __forceinline__ int32_t sample_pick(int env, const int32_t *__restric
                                                const int32_t *__restrict__ offsets, const int32_t *__restrict__ values,
                                                int64_t cap, uint64_t seed, uint64_t ply)
 {
-    const int c = Uniform ? uniform_word(counts + env) : counts[env];
+    int32_t c, o;
+    if (Uniform) {   // both words in one batch of scalar loads
+        c = uniform_word_raw(counts + env);
+        o = uniform_word_raw(offsets + env);
+        pin_word(c);
+        pin_word(o);
+    } else {
+        c = counts[env];
+        o = offsets[env];
+    }
     if (c <= 0) return -1;
-    const int64_t off = Uniform ? uniform_word(offsets + env) : offsets[env];
+    const int64_t off = o;
     if (off < 0 || off + c > cap) return -1;
     const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
                                      (uint32_t)seed, (uint32_t)(seed >> 32));
@@ -1521,15 +1537,13 @@ __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_
 // the largest u_c, ties to the smallest c: one 64-bit key (u_c, ~c) per lane,
 // maximised across the wave. Returns the world id (wave-uniform, -1 for an
 // empty or out-of-buffer row) and its canonical id in `canon`.
-__device__ __forceinline__ int32_t sample_logits_wave(int env, int l, int seat, const int32_t *__restrict__ counts,
-                                                      const int32_t *__restrict__ offsets,
+// `c` and `off` are the env's CSR count and offset (wave-uniform).
+__device__ __forceinline__ int32_t sample_logits_wave(int env, int l, int seat, int c, int64_t off,
                                                       const int32_t *__restrict__ values, int64_t cap, uint64_t seed,
                                                       uint64_t ply, int &canon)
 {
     canon = -1;
-    const int c = uniform_word(counts + env);
     if (c <= 0 || seat < 0 || seat > 3) return -1;
-    const int64_t off = uniform_word(offsets + env);
     if (off < 0 || off + c > cap) return -1;
     uint64_t best = 0;
     int32_t bw = -1;
@@ -1559,8 +1573,11 @@ __global__ __launch_bounds__(64) void k_sample_logits(State S, const int8_t *__r
     const int env = blockIdx.x, l = threadIdx.x;
     if (env >= S.n) return;
     const int seat = acting ? acting[env] : S.env[env].turn;
+    int32_t c = uniform_word_raw(counts + env), o = uniform_word_raw(offsets + env);
+    pin_word(c);
+    pin_word(o);
     int cc;
-    const int32_t a = sample_logits_wave(env, l, seat, counts, offsets, values, cap, seed, ply, cc);
+    const int32_t a = sample_logits_wave(env, l, seat, c, o, values, cap, seed, ply, cc);
     if (l == 0) {
         out[env] = a;
         if (canon_out) canon_out[env] = a >= 0 ? cc : -1;
@@ -1603,21 +1620,40 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
 {
     StepLoad ld;   // the ply's first loads go out before the sampler's
     step_load(S, env, l, ld);
+    // the env record and the CSR count and offset in one batch of scalar loads:
+    // one wait, then the sampler's only dependent load is its row of ids
+    const int32_t *ew = reinterpret_cast<const int32_t *>(S.env + env);
+    int32_t v[10];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = uniform_word_raw(ew + k);
+    const bool sampled = !A.actions;
+    v[8] = sampled ? uniform_word_raw(A.counts + env) : 0;
+    v[9] = sampled ? uniform_word_raw(A.offsets + env) : 0;
+#pragma unroll
+    for (int k = 0; k < 10; ++k) pin_word(v[k]);
+    EnvRec E0;
+    __builtin_memcpy(&E0, v, sizeof E0);
     int32_t a;
     if (A.actions) {
         a = A.actions[env];
     } else if (A.sampler == 1) {
         int cc;
-        a = sample_logits_wave(env, l, env_record(S, env).turn, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed,
-                               A.ply, cc);
+        a = sample_logits_wave(env, l, E0.turn, v[8], v[9], A.values, A.values_cap, A.sample_seed, A.ply, cc);
     } else {
-        a = sample_pick<true>(env, A.counts, A.offsets, A.values, A.values_cap, A.sample_seed, A.ply);
+        const int c = v[8];
+        const int64_t off = v[9];
+        a = -1;
+        if (c > 0 && off >= 0 && off + c <= A.values_cap) {
+            const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)A.ply, (uint32_t)(A.ply >> 32), 0u,
+                                             (uint32_t)A.sample_seed, (uint32_t)(A.sample_seed >> 32));
+            a = A.values[off + (int)(((uint64_t)u * (uint64_t)c) >> 32)];
+        }
     }
     if (A.actions_out && l == 0) A.actions_out[env] = a;
     TurnAfter nx;
     {
         StepRes res;
-        step_env(S, env, l, a, nullptr, 0, res, E.cell, E.pos, E.ptype, nx, &ld);
+        step_env(S, env, l, a, nullptr, 0, res, E.cell, E.pos, E.ptype, nx, &ld, &E0);
         if (l == 0) E.res = res;
     }
     wave_sync();
