@@ -15,7 +15,10 @@ from pathlib import Path
 import numpy as np
 
 _HERE = Path(__file__).resolve().parent
-LIB_PATH = _HERE / "_build" / "libjq_oracle.so"
+# JQ_ORACLE_LIB names another build of the oracle: the mutation tests load
+# copies with one planted mistake this way, to show the tests reject them.
+LIB_PATH = (Path(os.environ["JQ_ORACLE_LIB"]) if os.environ.get("JQ_ORACLE_LIB")
+            else _HERE / "_build" / "libjq_oracle.so")
 RECENCY_LUT_PATH = _HERE.parent / "tests" / "golden" / "recency_lut_f32.bin"
 
 NC = 289
