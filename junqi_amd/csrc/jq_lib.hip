@@ -585,9 +585,11 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
                            static_cast<uint8_t *>(aux), global, nrows);
         break;
     }
-    if ((rc = launch_check("k_observe")) != 0) return rc;
+    rc = launch_check("k_observe");
+    // the end event follows its begin event even when the launch failed, so no
+    // later launch is paired with it
     if (t_end) HIP_TRY(hipEventRecord(t_end, strm(stream)));
-    return JQ_OK;
+    return rc;
 }
 
 int jq_obs_timing(jq_env *e, int32_t enable)
