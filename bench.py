@@ -11,7 +11,10 @@ timed window holds openings, middle games and endgames, and games end and
 restart inside it.
 
 Prints one JSON line. Usage: python bench.py [--steps K] [--warmup W]
-  --config c5 (default): 32,768 games, logits sampler, step + CSR + mask + u8 obs
+  --config c5 (default): 32,768 games, logits sampler, step + CSR + mask + u8 obs;
+      the line's "dropin" object times the same workload a second time through
+      the reference collector's unchanged calls (f32 obs + bool mask; --no-dropin
+      skips it)
   --config c3: 16,384 games at plies 0-400, uniform sampler, step + CSR + mask + obs
   --config c2: 4,096 games, uniform sampler, step + CSR + mask (no observation)
   --path fused | separate | dropin (the reference collector's GpuRollout calls)
@@ -63,6 +66,8 @@ def parse():
     ap.add_argument("--cpu-envs", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="c5 fused only: skip the second timed run through GpuRollout's calls")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (counter calibration) and exit")
     return ap.parse_args()
@@ -150,14 +155,10 @@ def measured_traffic(kernel: str, games: int):
     return round(rec["read_bytes"] + rec["write_bytes"])
 
 
-def main() -> int:
-    args = parse()
-    if args.calibrate_copy:
-        return calibrate_copy(args.calibrate_copy)
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the environment shards by games with no exchange "
-              "(G GPUs = G independent batches), so it has no multi-GPU run", file=sys.stderr)
-        return 2
+def measure(args, path: str) -> dict:
+    """Play the batch into mixed stages, then time `args.steps` env-steps of
+    `path` (fused / separate / dropin); returns the JSON record without the CPU
+    baseline."""
     import numpy as np
     import torch
 
@@ -169,8 +170,8 @@ def main() -> int:
     sampler = args.sampler or cfg["sampler"]
     smp = L.SAMPLE_LOGITS if sampler == "logits" else L.SAMPLE_UNIFORM
     stagger = cfg["stagger"] if args.stagger < 0 else args.stagger
-    with_obs = cfg["obs"] or args.path == "dropin"
-    fmt = "f32" if args.path == "dropin" else args.fmt
+    with_obs = cfg["obs"] or path == "dropin"
+    fmt = "f32" if path == "dropin" else args.fmt
     b = junqi_amd.JunqiBatch(n, show_mode=args.show_mode, max_num_moves=4000, pool_size=10000)
     b.reset(0)
     b.legal()
@@ -187,7 +188,7 @@ def main() -> int:
     hsh = torch.empty((K + 1, n), dtype=torch.int64, device=dev)
     acts = torch.empty((K + 1, n), dtype=torch.int32, device=dev)
     canon = torch.empty(n, dtype=torch.int32, device=dev)
-    mask_bool = torch.empty((n, 16641), dtype=torch.uint8, device=dev) if args.path == "dropin" else None
+    mask_bool = torch.empty((n, 16641), dtype=torch.uint8, device=dev) if path == "dropin" else None
     h, lib = b._h, L.lib
     cap = b.values.numel()
     P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
@@ -212,7 +213,7 @@ def main() -> int:
 
     def one_step(ply: int, slot: int):
         s = torch.cuda.current_stream(dev).cuda_stream
-        if args.path == "fused":
+        if path == "fused":
             # one call: sample from the previous CSR rows, ply, restart, next seat's
             # CSR + mask, observation (the library times the observation kernel)
             L.check(lib.jq_env_step(h, None, smp, args.seed, ply, ply, b.counts.data_ptr(), b.offsets.data_ptr(),
@@ -220,7 +221,7 @@ def main() -> int:
                                     P(glob), term[slot].data_ptr(), reward[slot].data_ptr(), hsh[slot].data_ptr(),
                                     acts[slot].data_ptr(), s))
             return
-        if args.path == "separate":
+        if path == "separate":
             if smp == L.SAMPLE_LOGITS:
                 L.check(lib.jq_sample_logits(h, None, b.counts.data_ptr(), b.offsets.data_ptr(),
                                              b.values.data_ptr(), cap, args.seed, ply, acts[slot].data_ptr(), None, s))
@@ -271,8 +272,8 @@ def main() -> int:
 
     steps_per_s = n * K / (ms_total / 1e3)
     obs_bytes = (OBS_ELEMS * es + (AUX_BYTES if fmt == "u8" else 0) + GLOBAL_BYTES) if with_obs else 0
-    mask_bytes = 16641 if args.path == "dropin" else MASK_BYTES
-    step_bytes = obs_bytes + mask_bytes + 8 + 4 * kbar + (STEP_OUT_BYTES if args.path == "fused" else 5)
+    mask_bytes = 16641 if path == "dropin" else MASK_BYTES
+    step_bytes = obs_bytes + mask_bytes + 8 + 4 * kbar + (STEP_OUT_BYTES if path == "fused" else 5)
     whole = step_bytes * steps_per_s / 1e9
     rec = {
         "metric": METRIC,
@@ -289,10 +290,10 @@ def main() -> int:
         "data": "synthetic: seeded random legal setups, Philox-sampled legal actions, games played into mixed "
                 "stages before timing, auto-reset from a 10000-setup pool",
         "config": {"workload": f"{args.config}: sample ({sampler}) + step + pool restart + sorted legal CSR + "
-                               + ("bool canonical mask" if args.path == "dropin" else "packed canonical mask")
+                               + ("bool canonical mask" if path == "dropin" else "packed canonical mask")
                                + (f" + 317-plane {fmt} obs of the acting seat" if with_obs else "")
                                + f", {n} games, show mode {args.show_mode}",
-                   "games": n, "obs_format": fmt if with_obs else None, "path": args.path, "sampler": sampler,
+                   "games": n, "obs_format": fmt if with_obs else None, "path": path, "sampler": sampler,
                    "stagger_steps": stagger, "mean_legal_actions": round(kbar, 2),
                    "plies_at_start": {"min": int(plies0.min()), "mean": round(float(plies0.mean()), 1),
                                       "max": int(plies0.max())},
@@ -313,6 +314,32 @@ def main() -> int:
                            "frac": round(whole / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "whole step",
                            "kernel_ms": round(ms_total / K, 4), "bytes_per_launch": round(step_bytes * n)}
     b.close()
+    return rec
+
+
+def main() -> int:
+    args = parse()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the environment shards by games with no exchange "
+              "(G GPUs = G independent batches), so it has no multi-GPU run", file=sys.stderr)
+        return 2
+    import torch
+
+    rec = measure(args, args.path)
+    if args.path == "fused" and args.config == "c5" and not args.no_dropin:
+        # the same games through the reference collector's unchanged calls: f32
+        # observation, bool canonical mask, canonical step, device reset
+        torch.cuda.empty_cache()
+        d = measure(args, "dropin")
+        torch.cuda.empty_cache()
+        rec["dropin"] = {"value": d["value"], "unit": d["unit"], "ms_per_step": d["ms_per_step"], "dtype": d["dtype"],
+                         "workload": d["config"]["workload"], "steps": d["steps"], "warmup": d["warmup"],
+                         "roofline": {k: d["roofline"][k] for k in ("kernel", "kernel_ms", "achieved", "frac")},
+                         "whole_step": d["whole_step"]}
+    sampler = args.sampler or CONFIGS[args.config]["sampler"]
+    with_obs = CONFIGS[args.config]["obs"] or args.path == "dropin"
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline(args.cpu_envs, args.cpu_seconds, 1 if sampler == "logits" else 0,
                                            with_obs, args.seed)
