@@ -152,6 +152,25 @@ __device__ __forceinline__ void wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Streaming stores, for outputs that nothing in the same launch reads back.
+// Every launch ends by writing back the dirty lines of the XCDs' L2 caches, and
+// the next launch on the stream starts only after that: for a kernel that
+// streams gigabytes through L2 this writeback took ≈6 µs. With the
+// non-temporal hint the lines go out to memory as they are written and leave
+// little dirty data behind.
+template <typename T>
+__device__ __forceinline__ void stream_store(T *p, T v)
+{
+    __builtin_nontemporal_store(v, p);
+}
+
+__device__ __forceinline__ void stream_store(uint4 *p, uint4 v)
+{
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 x = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x4 *>(p));
+}
+
 __device__ __forceinline__ size_t cm_idx(int env, int o, int pid) { return ((size_t)env * 4 + o) * PID_STRIDE + pid; }
 __device__ __forceinline__ size_t pc_idx(int env, int pid) { return (size_t)env * PID_STRIDE + pid; }
 

@@ -613,6 +613,17 @@ __device__ __forceinline__ void obs_elems(const ObsLds &L, uint8_t *row, int e, 
     }
 }
 
+// A 16-byte chunk of a bf16 / f32 row. The bf16 rows go out as streaming
+// stores (1.464 -> 1.365 ms per fused bf16 step at 32,768 games); f32 rows
+// measured slower that way (2.68 -> 2.71 ms per drop-in step) and keep
+// ordinary stores.
+template <int FMT>
+__device__ __forceinline__ void row_store(uint4 *p, uint4 v)
+{
+    if constexpr (FMT == 1) stream_store(p, v);
+    else *p = v;
+}
+
 // Stream the 91,613-element row to `row` (element phase m) in 16-byte chunks:
 // chunk q covers row bytes [16q - lead, 16q - lead + 16). A wave iteration
 // stores one whole 1 KB-aligned unit of the buffer (the row's first and last
@@ -656,7 +667,7 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m, const ExtLds *X =
                                (obs_elem<FMT, EXT>(L, e0 + 2 * i + 1, m, X) << 16);
                     }
                 }
-                *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+                row_store<FMT>(reinterpret_cast<uint4 *>(dst), make_uint4(w[0], w[1], w[2], w[3]));
             }
             continue;
         }
@@ -679,7 +690,7 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m, const ExtLds *X =
             if (e0 < RG3_E && e0 + EPC > RG3_S) off = e0 + d3;
             out = obs_chunk<FMT>(L, e0, off, true);
         }
-        *reinterpret_cast<uint4 *>(dst) = out;
+        row_store<FMT>(reinterpret_cast<uint4 *>(dst), out);
     }
     // partial chunks at the two ends of the row
     if (threadIdx.x == 0 && lead) obs_elems<FMT, EXT>(L, row, 0, EPC - m, m, X);
@@ -764,7 +775,7 @@ __device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m
         if (g >= gA && g < gB) {
             const int q = (int)(g - gbase);
             const int e0 = q * 16 - m;
-            slot[q] = u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3));
+            stream_store(&slot[q], u8_chunk(L, e0, u8_img_off(e0, d0, d1, d2, d3)));
         }
     }
     // partial chunks at the two ends of the row
