@@ -137,7 +137,7 @@ def cpu_baseline(envs: int, seconds: float, sampler: int, obs: bool, seed: int) 
                       f"({work}, {'logits' if sampler else 'uniform'} sampler, HALF_DARK, after 64 untimed steps)"}
 
 
-OBS_TIMED_EVERY = 4   # observation launches timed with events: every 4th step of the timed region
+OBS_TIMED_EVERY = 8   # observation launches timed with events: every 8th step of the timed region
 
 # device kernel that writes the observation rows, per output format
 OBS_KERNEL = {"f32": "jq::k_observe<0, false>", "bf16": "jq::k_observe<1, false>", "u8": "jq::k_observe_u8_persist"}
@@ -256,7 +256,8 @@ def measure(args, path: str) -> dict:
     t_start.record()
     for k in range(K):
         # HIP events around the observation launch of every OBS_TIMED_EVERY-th step,
-        # on its stream (each pair costs the step about 6 us of queue time)
+        # on its stream (the end event costs that step about 6 us of queue time;
+        # the fused call's begin event doubles as the release of its side stream)
         L.check(lib.jq_obs_timing(h, 1 if k % OBS_TIMED_EVERY == 0 else 0))
         one_step(stagger + args.warmup + k, k)
     t_end.record()

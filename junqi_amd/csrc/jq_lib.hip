@@ -294,9 +294,10 @@ int obs_args(const jq_env *e, int32_t fmt, const void *spatial, const void *aux,
 
 // With jq_obs_timing on: record the begin event of the next observation launch
 // on `stream` and hand back its end event (else *t_end = nullptr).
-int obs_timing_begin(jq_env *e, void *stream, hipEvent_t *t_end)
+int obs_timing_begin(jq_env *e, void *stream, hipEvent_t *t_end, hipEvent_t *t_begin = nullptr)
 {
     *t_end = nullptr;
+    if (t_begin) *t_begin = nullptr;
     if (!e->obs_timing || e->obs_ev_used >= JQ_OBS_TIMING_MAX) return JQ_OK;
     if (e->obs_ev_used == e->obs_ev.size()) {   // a pair per launch, reused after jq_obs_timing_read
         hipEvent_t a = nullptr, b = nullptr;
@@ -310,6 +311,7 @@ int obs_timing_begin(jq_env *e, void *stream, hipEvent_t *t_end)
     const auto &pr = e->obs_ev[e->obs_ev_used++];
     HIP_TRY(hipEventRecord(pr.first, strm(stream)));
     *t_end = pr.second;
+    if (t_begin) *t_begin = pr.first;
     return JQ_OK;
 }
 
@@ -716,9 +718,11 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
             HIP_TRY(hipEventCreateWithFlags(&e->ev_step, hipEventDisableTiming));
             HIP_TRY(hipEventCreateWithFlags(&e->ev_csr, hipEventDisableTiming));
         }
-        // a timing event goes before the release of the side stream, so the
-        // observation's dispatch still follows the step directly
-        if ((rc = obs_timing_begin(e, stream, &e->obs_t_end)) != 0) return rc;
+        // Each event between two kernels of a stream holds the second back by
+        // ≈6 µs, so a timed step's begin event also releases the side stream;
+        // an untimed step records the release event alone.
+        hipEvent_t t_begin = nullptr;
+        if ((rc = obs_timing_begin(e, stream, &e->obs_t_end, &t_begin)) != 0) return rc;
         // Whatever path leaves this block, an end event whose begin was recorded
         // above and that the observation did not take is recorded here, so no
         // later launch pairs with it.
@@ -732,8 +736,8 @@ int jq_env_step(jq_env *e, const int32_t *actions, int32_t sampler, uint64_t sam
                 }
             }
         } close_timing{e, stream};
-        HIP_TRY(hipEventRecord(e->ev_step, strm(stream)));
-        HIP_TRY(hipStreamWaitEvent(e->side, e->ev_step, 0));
+        if (!t_begin) HIP_TRY(hipEventRecord(e->ev_step, strm(stream)));
+        HIP_TRY(hipStreamWaitEvent(e->side, t_begin ? t_begin : e->ev_step, 0));
         hipLaunchKernelGGL(k_scan, dim3(1), dim3(SCAN_THREADS), 0, e->side, counts, offsets, e->S.n);
         if ((rc = launch_check("k_scan")) != 0) return rc;
         hipLaunchKernelGGL(k_emit, dim3((e->S.n + 1) / 2), dim3(64), 0, e->side, e->S, offsets, values,
