@@ -1380,7 +1380,7 @@ __global__ __launch_bounds__(64) void k_emit(State S, const int32_t *__restrict_
             const int c0 = __popcll(w0), c1 = __popcll(w1);
             const int c = k < c0 ? select64(w0, k)
                                  : k < c0 + c1 ? 64 + select64(w1, k - c0) : 128 + select64(w2, k - c0 - c1);
-            if (base >= 0 && (int64_t)base + i < cap) stream_store(values + base + i, s * NC + c2f[c]);
+            if (base >= 0 && (int64_t)base + i < cap) values[base + i] = s * NC + c2f[c];
             if (mask_words) {   // canonical bit (rotated source) * 129 + (rotated destination)
                 const int bit = cs * NONB + rot[h][c];
                 atomicOr(&mbits[h][bit >> 5], 1u << (bit & 31));
