@@ -647,7 +647,9 @@ __device__ void obs_emit(const ObsLds &L, uint8_t *row, int m, const ExtLds *X =
     const int nu = (int)(u1 - u0);
     const int per = (nu + NW - 1) / NW;
     const int ka = min(nu, wv * per), kb = min(nu, ka + per);
-    for (int k = ka; k < kb; ++k) {
+    const bool back = wv & 1;   // odd waves walk their run from its end, as in obs_emit_u8
+    for (int i = ka; i < kb; ++i) {
+        const int k = back ? ka + kb - 1 - i : i;
         const int qb = (int)((int64_t)((u0 + k) << 6) - (int64_t)gbase);
         const int s_lo = max(qb, qf) * EPC - m, s_hi = min(qb + 64, ql) * EPC - m;
         const int q = qb + lane;
@@ -770,7 +772,13 @@ __device__ __forceinline__ void obs_emit_u8(const ObsLds &L, uint8_t *row, int m
     const int nu = (int)(u1 - u0);
     const int per = (nu + NW - 1) / NW;
     const int ka = min(nu, wv * per), kb = min(nu, ka + per);
-    for (int k = ka; k < kb; ++k) {
+    // Odd waves walk their run from its end: the runs of waves 1 and 2 (and of
+    // wave 3 and the next row's wave 0) start side by side and those of waves 0
+    // and 1 (2 and 3) end side by side (0.7601 -> 0.7528 ms per fused step at
+    // 32,768 games; every wave walking backward 0.7635).
+    const bool back = wv & 1;
+    for (int i = ka; i < kb; ++i) {
+        const int k = back ? ka + kb - 1 - i : i;
         const uint64_t g = ((u0 + k) << 6) + lane;
         if (g >= gA && g < gB) {
             const int q = (int)(g - gbase);
