@@ -88,6 +88,28 @@ def calibrate_copy(mb: int) -> int:
     return 0
 
 
+def fill_rate_gbps(nbytes: int, reps: int = 5) -> float:
+    """Best write rate of a plain device fill of `nbytes` (torch's fill kernel
+    on the current stream, timed with events): the practical ceiling of a
+    kernel that only writes, measured on the same device."""
+    import torch
+
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        buf.fill_(1)
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        buf.fill_(2)
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1))
+    del buf
+    torch.cuda.empty_cache()
+    return nbytes / (best / 1e3) / 1e9
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -315,6 +337,12 @@ def measure(args, path: str) -> dict:
                            "frac": round(whole / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "whole step",
                            "kernel_ms": round(ms_total / K, 4), "bytes_per_launch": round(step_bytes * n)}
     b.close()
+    if with_obs:
+        # the same byte count written by a plain device fill: what a write-only
+        # kernel can reach on this device, beside the 8 TB/s spec peak
+        fill = fill_rate_gbps(per_launch)
+        rec["roofline"]["measured_fill_GBps"] = round(fill, 1)
+        rec["roofline"]["frac_of_fill"] = round(rec["roofline"]["achieved"] / fill, 4)
     return rec
 
 
