@@ -1494,42 +1494,27 @@ __device__ __forceinline__ uint32_t philox4x32_10(uint32_t c0, uint32_t c1, uint
     return c0;
 }
 
-// Uniform pick from env's CSR row: Philox4x32-10 word 0 of counter
-// (env, ply lo, ply hi, 0) under key (seed lo, seed hi), scaled to the count;
-// -1 for an empty row or one that does not lie inside the values buffer.
-// Uniform: env is the same on every lane of the wave (one env per wave), so the
-// count and offset are scalar loads; else one env per lane.
-template <bool Uniform>
-__device__ __forceinline__ int32_t sample_pick(int env, const int32_t *__restrict__ counts,
-                                               const int32_t *__restrict__ offsets, const int32_t *__restrict__ values,
-                                               int64_t cap, uint64_t seed, uint64_t ply)
+// Uniform pick from env's CSR row of c ids at offset off: Philox4x32-10 word 0
+// of counter (env, ply lo, ply hi, 0) under key (seed lo, seed hi), scaled to
+// the count; -1 for an empty row or one that does not lie inside the values
+// buffer.
+__device__ __forceinline__ int32_t uniform_pick(int env, int c, int64_t off, const int32_t *__restrict__ values,
+                                                int64_t cap, uint64_t seed, uint64_t ply)
 {
-    int32_t c, o;
-    if (Uniform) {   // both words in one batch of scalar loads
-        c = uniform_word_raw(counts + env);
-        o = uniform_word_raw(offsets + env);
-        pin_word(c);
-        pin_word(o);
-    } else {
-        c = counts[env];
-        o = offsets[env];
-    }
-    if (c <= 0) return -1;
-    const int64_t off = o;
-    if (off < 0 || off + c > cap) return -1;
+    if (c <= 0 || off < 0 || off + c > cap) return -1;
     const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)ply, (uint32_t)(ply >> 32), 0u,
                                      (uint32_t)seed, (uint32_t)(seed >> 32));
-    const int idx = (int)(((uint64_t)u * (uint64_t)c) >> 32);
-    return values[off + idx];
+    return values[off + (int)(((uint64_t)u * (uint64_t)c) >> 32)];
 }
 
+// One env per thread.
 __global__ void k_sample(int n, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
                          const int32_t *__restrict__ values, int64_t cap, uint64_t seed, uint64_t ply,
                          int32_t *__restrict__ out)
 {
     const int env = blockIdx.x * blockDim.x + threadIdx.x;
     if (env >= n) return;
-    out[env] = sample_pick<false>(env, counts, offsets, values, cap, seed, ply);
+    out[env] = uniform_pick(env, counts[env], offsets[env], values, cap, seed, ply);
 }
 
 // Masked-logit pick by env's wave (lane l): the legal ids of the CSR row, lane
@@ -1642,14 +1627,7 @@ __device__ __forceinline__ void env_step_wave(const State &S, int env, int l, co
         int cc;
         a = sample_logits_wave(env, l, E0.turn, v[8], v[9], A.values, A.values_cap, A.sample_seed, A.ply, cc);
     } else {
-        const int c = v[8];
-        const int64_t off = v[9];
-        a = -1;
-        if (c > 0 && off >= 0 && off + c <= A.values_cap) {
-            const uint32_t u = philox4x32_10((uint32_t)env, (uint32_t)A.ply, (uint32_t)(A.ply >> 32), 0u,
-                                             (uint32_t)A.sample_seed, (uint32_t)(A.sample_seed >> 32));
-            a = A.values[off + (int)(((uint64_t)u * (uint64_t)c) >> 32)];
-        }
+        a = uniform_pick(env, v[8], v[9], A.values, A.values_cap, A.sample_seed, A.ply);
     }
     if (A.actions_out && l == 0) A.actions_out[env] = a;
     TurnAfter nx;

@@ -28,6 +28,7 @@ struct jq_env {
     std::vector<void *> allocs;
     bool zob_ready = false, rlut_ready = false;
     int obs_blocks = 0;              // resident u8 observation blocks on the device
+    int obs_f32_pad = -1;            // dynamic LDS bytes that hold the f32 observation at 3 blocks per CU
     float *ext_bel = nullptr;        // uploaded (N, 4, 12, 289) beliefs, allocated on first upload
     bool ext_on = false;             // observations read the uploaded beliefs
     int8_t *pool = nullptr;          // setup pool buffer (reused while uploads fit)
@@ -273,6 +274,35 @@ int obs_u8_grid(jq_env *e)
     HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_observe_u8_persist, OBS_THREADS, 0));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
     e->obs_blocks = std::max(1, per_cu) * std::max(1, cus);
+    return JQ_OK;
+}
+
+// The f32 observation (one block per 366,452-byte row) writes faster with at
+// most 3 blocks per CU than at the 4 its LDS and registers allow (fewer rows
+// streaming at once: 2.377 -> 2.272 ms per launch at 32,768 rows; bf16 rows,
+// half as long, are slower at 3). Each block asks for unused dynamic LDS that
+// brings it to the midpoint between a third and a quarter of the CU's LDS, so
+// a fourth block does not fit and a third still does after the allocation
+// rounds up (a pad that left only 0.9 % of slack under the third was rounded
+// past it: 2 blocks per CU, 3.06 ms). 0 when the occupancy query does not
+// confirm exactly 3.
+int obs_f32_pad(jq_env *e, int &pad)
+{
+    if (e->obs_f32_pad < 0) {
+        hipFuncAttributes fa{};
+        int lds_cu = 0, per_cu = 0;
+        HIP_TRY(hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&k_observe<0, false>)));
+        HIP_TRY(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, e->device));
+        int p = (lds_cu / 3 + lds_cu / 4) / 2 - (int)fa.sharedSizeBytes;
+        if (p > 0) {
+            HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_observe<0, false>, OBS_THREADS, p));
+            if (per_cu != 3) p = 0;
+        } else {
+            p = 0;
+        }
+        e->obs_f32_pad = p;
+    }
+    pad = e->obs_f32_pad;
     return JQ_OK;
 }
 
@@ -565,6 +595,8 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
     const dim3 grid(nrows), block(OBS_THREADS);
     const float *x = e->ext_bel;
     if (fmt == JQ_OBS_U8 && (rc = obs_u8_grid(e)) != 0) return rc;
+    int f32_pad = 0;
+    if (fmt == JQ_OBS_F32 && !e->ext_on && (rc = obs_f32_pad(e, f32_pad)) != 0) return rc;
     hipEvent_t t_end = e->obs_t_end;   // begin already recorded by jq_env_step
     e->obs_t_end = nullptr;
     if (!t_end && (rc = obs_timing_begin(e, stream, &t_end)) != 0) return rc;
@@ -573,7 +605,7 @@ int jq_observe(jq_env *e, const int8_t *observer, int32_t fmt, int32_t all_seats
         if (e->ext_on)
             hipLaunchKernelGGL((k_observe<0, true>), grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, x);
         else
-            hipLaunchKernelGGL((k_observe<0, false>), grid, block, 0, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, nullptr);
+            hipLaunchKernelGGL((k_observe<0, false>), grid, block, f32_pad, strm(stream), e->S, observer, all_seats, spatial, aux, global, nrows, nullptr);
         break;
     case JQ_OBS_BF16:
         if (e->ext_on)
