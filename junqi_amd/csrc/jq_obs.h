@@ -823,6 +823,10 @@ __global__ __launch_bounds__(OBS_THREADS) void k_observe(State S, const int8_t *
     row_fill<EXT, FMT == 2>(S, obs, m, t, R, L, glob ? glob + (size_t)row * 28 : nullptr,
                             EXT ? ext + ((size_t)env * 4 + obs) * 12 * NC : nullptr, X);
     lds_barrier();
+    // f32 rows: a short sleep between the fill and the stores (s_sleep 1, 2 or 4:
+    // 2.271 -> 2.230-2.237 ms per launch at 32,768 rows, three alternations;
+    // 8 / 16 / 32 2.239 / 2.249 / 2.259; bf16 and u8 rows gain nothing)
+    if (FMT == 0) __builtin_amdgcn_s_sleep(2);
     if (FMT == 2) obs_emit_u8(L, rowp, m, aux ? static_cast<uint8_t *>(aux) + (size_t)row * AUXC_ROW : nullptr, t);
     else obs_emit<FMT, EXT>(L, rowp, m, X);
 }
