@@ -1199,6 +1199,7 @@ __device__ __forceinline__ void legal_body(const State &S, int env, int l, int s
     if (mask_words)
         for (int w = l; w < JQ_MASK_WORDS; w += 64) mask_words[(size_t)env * JQ_MASK_WORDS + w] = (int32_t)bits[w];
     if (mask_bool) {
+        __builtin_amdgcn_s_setprio(0);
         uint8_t *row = mask_bool + (size_t)env * JQ_ACTION_DIM;
         // bytes until the first 16-byte boundary, then whole 16-byte chunks, then the tail
         const int mis = (int)((uintptr_t)row & 15);
@@ -1228,6 +1229,11 @@ __global__ __launch_bounds__(64) void k_legal(State S, const int8_t *__restrict_
     const int seat = acting ? acting[env] : E.turn;
     const bool off = E.term || seat < 0 || seat > 3 || ((E.sdead >> (seat & 3)) & 1);
     for (int f = l; f < CELL_STRIDE; f += 64) cell[f] = f < NC ? S.cell[(size_t)env * CELL_STRIDE + f] : -1;
+    // wave issue priority 2 through the legal pass, 0 for the bool rows'
+    // stores (legal_body lowers it): a wave still computing gets issue slots
+    // ahead of the waves that are storing rows (drop-in step at 32,768 games:
+    // 2.486 -> 2.474 ms)
+    __builtin_amdgcn_s_setprio(2);
     for (int w = l; w < JQ_MASK_WORDS_PAD; w += 64) bits[w] = 0;
     if (mask_words || mask_bool) {
         const int s4 = seat & 3;
